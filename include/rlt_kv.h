@@ -1,0 +1,234 @@
+/*
+ * rlt_kv: C ABI of the MI355X (gfx950) depth-aware paged-KV hot path.
+ *
+ * Every buffer is caller-owned device memory passed as a raw pointer; the
+ * library never allocates or frees device memory and never synchronises the
+ * host.  All work is enqueued on the caller's HIP stream (`stream`, a
+ * hipStream_t passed as void*; NULL is the default stream).
+ *
+ * Strides are in ELEMENTS, not bytes, and are 64-bit everywhere: a block id
+ * multiplied by a block stride is computed in int64 before any addition, so
+ * pools whose element offsets exceed 2^31 (or byte offsets above 2^32) are
+ * addressed correctly.
+ *
+ * Pool layout (per tensor, K and V identical):
+ *   [num_blocks, num_layers, page_size, num_kv_heads, head_dim]
+ * as created by vllm_rlt/core/kv_cache_manager.py:132-134.  A "layer slice"
+ * is key_cache[:, layer], i.e. [num_blocks, page_size, num_kv_heads, head_dim]
+ * with the pool's block stride.
+ *
+ * Return value of every entry point: RLT_OK (0) on success, a negative
+ * rlt_status otherwise.  rlt_last_error() returns a message for the calling
+ * thread's last failure.  RLT_EINVAL means nothing was enqueued.
+ */
+#ifndef RLT_KV_H
+#define RLT_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  RLT_OK = 0,
+  RLT_EINVAL = -1,      /* invalid argument; nothing enqueued */
+  RLT_EUNSUPPORTED = -2, /* valid but unsupported shape/dtype; nothing enqueued */
+  RLT_ELAUNCH = -3,     /* the HIP runtime rejected a launch */
+  RLT_EWORKSPACE = -4   /* workspace too small; nothing enqueued */
+} rlt_status;
+
+/* Storage dtypes accepted for K/V/q/out (vllm_rlt/core/kv_cache_manager.py:111-112). */
+typedef enum { RLT_FLOAT32 = 0, RLT_FLOAT16 = 1, RLT_BFLOAT16 = 2 } rlt_dtype;
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char* rlt_last_error(void);
+
+/* Library version string, e.g. "rlt_kv 0.1 gfx950". */
+const char* rlt_version(void);
+
+/*
+ * KV append / scatter of one layer.
+ * Replaces the two index_put launches of _write_prepared
+ *   vllm_rlt/core/kv_cache_manager.py:531-532
+ * and the captured equivalent in vllm_rlt/worker/cuda_graph.py:16-20:
+ *   key_cache[write_blocks[i], layer, write_offsets[i]]   = k[i]
+ *   value_cache[write_blocks[i], layer, write_offsets[i]] = v[i]
+ * for i < n_rows (padding rows beyond n_rows are never written).  A bitwise
+ * copy; the caller guarantees (block, offset) pairs are distinct
+ * (kv_cache_manager.py:416-419).
+ *   cache_strides[5]: block, layer, token, head, dim strides of key/value cache
+ *   k_strides[3], v_strides[3]: row, head, dim strides of k / v ([n, hkv, d]).
+ *   write_blocks, write_offsets: device int64 [n_rows].
+ */
+int rlt_kv_append(void* key_cache, void* value_cache, const int64_t* cache_strides,
+                  const void* k, const int64_t* k_strides, const void* v,
+                  const int64_t* v_strides, const int64_t* write_blocks,
+                  const int64_t* write_offsets, int64_t n_rows, int64_t layer,
+                  int64_t num_layers, int64_t num_blocks, int64_t page_size,
+                  int64_t num_kv_heads, int64_t head_dim, int dtype, void* stream);
+
+/*
+ * Workspace bytes rlt_paged_decode needs for n_rows rows.  Depends only on the
+ * shape, never on context lengths, so a caller can size it without a sync.
+ */
+int64_t rlt_paged_decode_workspace_bytes(int64_t n_rows, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t head_dim);
+
+/*
+ * Single-query paged GQA decode attention over per-row block tables.
+ * Replaces the attention callable contract
+ *   attention(q, key_cache, value_cache, block_tables, context_lengths)
+ * of vllm_rlt/kernels/paged_attention.py:12-36 (torch reference),
+ * vllm_rlt/kernels/triton_attention.py:100-125 (Triton) and
+ * vllm_rlt/kernels/flash_attention.py:98-130 (FlashAttention decode).
+ * Row r attends q[r, hq, :] to tokens 0..context_lengths[r]-1 of its table;
+ * q head j uses KV head j / (num_q_heads / num_kv_heads).  Softmax and both
+ * products accumulate in fp32 with scale applied to q.k; the output is
+ * rounded (nearest-even) to the storage dtype.  context_lengths[r] == 0 gives
+ * an all-zero row.  Table entries at index >= ceil(len / page_size) are never
+ * read, so padding may be -1 or 0.
+ *   q_strides[3], out_strides[3]: row, head, dim strides.
+ *   kv_strides[4]: block, token, head, dim strides of the LAYER SLICE; key and
+ *     value slices must share them.  key_cache/value_cache point at the slice.
+ *   block_tables: device int32 [n_rows, >= ceil(max_len/page)], row stride
+ *     table_stride.  context_lengths: device int32 [n_rows].
+ *   max_table_width: block_tables' column count; bounds the launch grid, and a
+ *     length above max_table_width * page_size is clamped to it.
+ *   workspace: device memory of >= rlt_paged_decode_workspace_bytes() bytes.
+ * Results are independent of batch composition: a row's output bits depend
+ * only on that row's inputs.
+ */
+int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
+                     const void* value_cache, const int64_t* kv_strides,
+                     const int32_t* block_tables, int64_t table_stride,
+                     int64_t max_table_width, const int32_t* context_lengths, void* out,
+                     const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
+                     int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                     int64_t num_blocks, float scale, int dtype, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes rlt_paged_prefill needs (shape-only, no sync needed). */
+int64_t rlt_paged_prefill_workspace_bytes(int64_t total_q, int64_t num_seqs,
+                                          int64_t max_table_width, int64_t num_q_heads,
+                                          int64_t num_kv_heads, int64_t head_dim);
+
+/*
+ * Packed chunked-prefill attention over paged prefixes, bottom-right causal.
+ * Replaces FlashPagedAttention.prefill, vllm_rlt/kernels/flash_attention.py:
+ * 66-96 (FA4 varlen with cu_seqlens_q, seqused_k, page_table, causal=True),
+ * selected by _attend_prepared when the batch carries cu_seqlens_q
+ * (vllm_rlt/core/kv_cache_manager.py:570-579).  Sequence s owns query rows
+ * [cu_seqlens_q[s], cu_seqlens_q[s+1]) of q and attends through
+ * block_tables[s]; context_lengths[s] is its key length (prefix + chunk), so
+ * query row i sees the first context_lengths[s] - (cu[s+1] - 1 - i) keys.
+ * The chunk's own K/V must already be in the pool.
+ *   cu_seqlens_q: device int32 [num_seqs + 1], cu[0] == 0, cu[num_seqs] == total_q.
+ *   block_tables: device int32 [num_seqs, max_table_width] (row stride table_stride).
+ */
+int rlt_paged_prefill(const void* q, const int64_t* q_strides, const void* key_cache,
+                      const void* value_cache, const int64_t* kv_strides,
+                      const int32_t* block_tables, int64_t table_stride,
+                      int64_t max_table_width, const int32_t* context_lengths,
+                      const int32_t* cu_seqlens_q, int64_t num_seqs, int64_t total_q,
+                      int64_t max_seqlen_q, void* out, const int64_t* out_strides,
+                      int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                      int64_t page_size, int64_t num_blocks, float scale, int dtype,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Batched LAST-EXITED exit copies from device-resident descriptors.
+ * Replaces finalize_kernel, vllm_rlt/kernels/routing.py:80-109 (launched at
+ * vllm_rlt/worker/model_runner.py:543-557).  For every descriptor i with
+ * (slot, depth, pos) = descriptors[3i .. 3i+2] and every target plane
+ * depth < target < max_loops, copies the token's K and V at ALL layers:
+ *   src = tables[(slot*planes + depth )*table_width + pos/page_size]
+ *   dst = tables[(slot*planes + target)*table_width + pos/page_size]
+ *   cache[dst, :, pos % page_size] = cache[src, :, pos % page_size]
+ *   descriptors: device (or device-visible pinned) int64 [n, 3].
+ *   tables: device int32 [num_slots, planes, table_width].
+ * Descriptors whose slot, page or table entries fall outside the tables or
+ * the pool are skipped (never dereferenced).
+ */
+int rlt_kv_finalize(const int64_t* descriptors, int64_t n, const int32_t* tables,
+                    int64_t table_width, int64_t planes, int64_t num_slots,
+                    void* key_cache, void* value_cache, const int64_t* cache_strides,
+                    int64_t num_layers, int64_t num_blocks, int64_t num_kv_heads,
+                    int64_t head_dim, int64_t page_size, int64_t max_loops, int dtype,
+                    void* stream);
+
+/*
+ * Synchronous exit copy of one token with host-known pages.
+ * Replaces the basic-index copies of finalize_token,
+ * vllm_rlt/core/kv_cache_manager.py:601-611:
+ *   cache[dst_blocks[j], :, offset] = cache[src_block, :, offset], j < n_dst
+ * dst_blocks is a HOST array (n_dst <= 64) passed by value in the launch, so
+ * no host-to-device index upload precedes the copy.
+ */
+int rlt_kv_copy_token(void* key_cache, void* value_cache, const int64_t* cache_strides,
+                      int64_t src_block, const int64_t* dst_blocks, int64_t n_dst,
+                      int64_t offset, int64_t num_layers, int64_t num_blocks,
+                      int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int dtype,
+                      void* stream);
+
+/*
+ * Gather one (request, plane, layer) history in position order.
+ * Replaces read(), vllm_rlt/core/kv_cache_manager.py:616-637:
+ *   out_k[t] = key_cache[table[t / page], layer, t % page], t < length
+ * (same for V).  table: device int32; out_k/out_v: contiguous
+ * [length, num_kv_heads, head_dim].
+ */
+int rlt_kv_gather(const void* key_cache, const void* value_cache,
+                  const int64_t* cache_strides, int64_t layer, const int32_t* table,
+                  int64_t length, void* out_k, void* out_v, int64_t num_layers,
+                  int64_t num_blocks, int64_t page_size, int64_t num_kv_heads,
+                  int64_t head_dim, int dtype, void* stream);
+
+/*
+ * GPU-resident decode metadata from (slot, depth, pos) descriptors.
+ * Replaces metadata_kernel, vllm_rlt/kernels/routing.py:8-41 (launched at
+ * vllm_rlt/worker/async_state.py:59-75).  For row < size:
+ *   valid = row < count;  (slot, depth, pos) = valid ? descriptors[3row..] : 0
+ *   plane = planes > 1 ? depth : 0;  base = (slot*planes + plane)*table_width
+ *   slots[row] = slot; positions[row] = pos; lengths[row] = valid ? pos+1 : 0
+ *   if valid: blocks[row] = tables[base + pos/page]; offsets[row] = pos % page
+ *   out_tables[row*out_table_stride + c] = valid ? tables[base + c] : 0,
+ *     c < out_width
+ * tables: device int32 [num_slots, planes, table_width].  A descriptor whose
+ * slot, plane or page lies outside the tables is handled like a padding row
+ * (length 0, zero table row, no write address) after slots/positions store it.
+ */
+int rlt_build_decode_metadata(const int64_t* descriptors, int64_t count, int64_t size,
+                              const int32_t* tables, int64_t num_slots,
+                              int64_t table_width, int64_t planes,
+                              int64_t page_size, int64_t* slots, int64_t* positions,
+                              int32_t* lengths, int64_t* blocks, int64_t* offsets,
+                              int32_t* out_tables, int64_t out_table_stride,
+                              int64_t out_width, void* stream);
+
+/*
+ * Stage a packed int64 blob into device int64 and int32 copies.
+ * Replaces stage_prefill, vllm_rlt/kernels/prefill_metadata.py:8-12.
+ * source may be device memory or device-visible pinned host memory.
+ */
+int rlt_stage_prefill(const int64_t* source, int64_t* target, int32_t* target32,
+                      int64_t n, void* stream);
+
+/*
+ * Expand packed prefill (position, sequence) pairs into write addresses.
+ * Replaces expand_prefill, vllm_rlt/kernels/prefill_metadata.py:16-32:
+ *   blocks[i] = tables[sequences[i]*table_width + positions[i]/page]
+ *   offsets[i] = positions[i] % page
+ * tables: device int32 [num_sequences, table_width]; an entry outside the
+ * tables yields block -1.
+ */
+int rlt_expand_prefill(const int64_t* positions, const int64_t* sequences,
+                       const int32_t* tables, int64_t num_sequences, int64_t table_width,
+                       int64_t page_size, int64_t* blocks, int64_t* offsets, int64_t n,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLT_KV_H */

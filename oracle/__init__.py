@@ -1,0 +1,29 @@
+"""CPU oracle for the depth-aware paged-KV path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product (vllm-rlt_amd/) imports,
+links or runs this package.  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may use it, and only as the checker (or, in the
+bench, as the timed CPU baseline) -- never as the thing measured on the GPU.
+
+Contents and what pins each function (see tests/test_oracle.py):
+
+* paged_attention.paged_attention_cpu -- op-for-op restatement of the
+  reference's CPU attention path, vllm_rlt/kernels/paged_attention.py:12-36.
+  Pinned by: textbook SDPA (torch.nn.functional.scaled_dot_product_attention),
+  an independent float64 numpy evaluation, the reference's known answers
+  (uniform q gives mean(V), tests/test_kv_cache.py:61-78; the worked examples
+  20 / 22.6894 / 20.73 of docs/kv_layout_computation.md:85,109,178; the exact
+  64-bit-offset answer arange(16), tests/test_attention_64bit.py:16-30) and
+  len == 0 -> zeros (paged_attention.py:25-27).
+* paged_attention.dense_attention -- the reference tests' dense oracle
+  (tests/test_attention.py:8-15), pinned against the f64 evaluation.
+* kv_ops.* -- numpy restatements of the byte/integer work: append scatter
+  (kv_cache_manager.py:531-532), exit copies (kv_cache_manager.py:601-611,
+  kernels/routing.py:80-109), ordered gather (kv_cache_manager.py:616-637),
+  decode metadata (kernels/routing.py:8-41), packed-prefill staging and
+  expansion (kernels/prefill_metadata.py:8-32) and the address/table rules of
+  _prepare_batch (kv_cache_manager.py:398-478).  Pinned by the reference's
+  golden vectors (tests/test_prepared_kv.py:49-53, tests/test_flash_attention.py:
+  134-137, tests/test_cdb_runtime.py:152-177, tests/test_async_state.py:152-164,
+  tests/test_kv_cache.py:38-59) and by brute-force invariants on small pools.
+"""

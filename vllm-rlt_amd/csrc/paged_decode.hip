@@ -1,0 +1,586 @@
+// Single-query paged GQA decode attention for gfx950.
+//
+// Work decomposition.  A row's context [0, len) is cut into fixed splits of
+// kSplitTokens tokens (rows longer than kMaxSplits splits use longer splits,
+// rounded to kSplitAlign).  The split plan of a row depends only on that
+// row's length, so a row's output bits never depend on the rest of the batch.
+// One wavefront processes one (row, kv_head, split) item; the four waves of a
+// workgroup are independent workers that walk the compact item list
+// (rows x splits x kv_heads, kv_head innermost so neighbouring waves read
+// neighbouring 256-byte head slices of the same token rows) in grid-stride
+// order.  Each workgroup first builds the exclusive prefix of split counts
+// over rows in LDS, so no host-side length information and no second launch
+// is needed to enumerate the ragged work.
+//
+// Inside an item.  Lanes form 64/LPT token groups of LPT lanes; lane (g, s)
+// owns dims [s*EPL, s*EPL+EPL) of tokens g, g+TPI, ... of every tile.  One
+// load instruction therefore reads TPI consecutive tokens that all lie in the
+// same page, so the page's base address is wave-uniform: the split's table
+// entries are fetched once (one per lane) and picked out with readlane, and
+// K/V move as global_load_dwordx4 with an SGPR page base.  Each lane group keeps its own
+// running max / normaliser / accumulator (exp2 domain, fp32), so a tile needs
+// no cross-group traffic; the groups are merged once per item.  Tokens past
+// the split end re-read the split's last valid token (in bounds, finite) and
+// are masked to probability 0, so table entries past ceil(len/page) are never
+// read and uninitialised pool memory never reaches the arithmetic.  A length
+// larger than the table covers is clamped to it.
+//
+// Multi-split rows write (max, sum, unnormalised acc) partials to the
+// workspace; a second kernel merges them in split order.  Single-split rows
+// write their output directly; empty rows are zeroed by the merge kernel.
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace rlt {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kSplitTokens = 256;
+constexpr int kMaxSplits = 64;
+constexpr int kSplitAlign = 64;
+constexpr int kMaxRowsPerLaunch = 8192;
+constexpr int kMaxGrid = 4096;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__host__ __device__ inline void split_plan(int len, int* split_len, int* nsplit) {
+  if (len <= 0) {
+    *split_len = kSplitTokens;
+    *nsplit = 0;
+    return;
+  }
+  const int n = (len + kSplitTokens - 1) / kSplitTokens;
+  if (n <= kMaxSplits) {
+    *split_len = kSplitTokens;
+    *nsplit = n;
+    return;
+  }
+  int per = (len + kMaxSplits - 1) / kMaxSplits;
+  per = (per + kSplitAlign - 1) / kSplitAlign * kSplitAlign;
+  *split_len = per;
+  *nsplit = (len + per - 1) / per;
+}
+
+struct DecodeArgs {
+  const void* q;
+  int64_t q_row, q_head, q_dim;
+  const void* k;
+  const void* v;
+  int64_t kv_block, kv_token, kv_head, kv_dim;
+  const int32_t* tables;
+  int64_t table_stride;
+  const int32_t* lens;
+  void* out;
+  int64_t o_row, o_head, o_dim;
+  float* ws_acc;  // [rows][hkv][kMaxSplits][G][D]
+  float2* ws_ml;  // [rows][hkv][kMaxSplits][G]  (max in log2 units, sum)
+  int n_rows, hkv, hq, d, page;
+  int64_t num_blocks;
+  int64_t max_len;  // table width * page: lengths are clamped to what the table covers
+  float qscale;     // softmax scale * log2(e)
+};
+
+// A row's effective context length; never reaches past its table row.
+__device__ __forceinline__ int row_length(const DecodeArgs& a, int r) {
+  const int64_t len = a.lens[r];
+  return static_cast<int>(len < a.max_len ? len : a.max_len);
+}
+
+// Builds prefix[0..n] = exclusive scan of split counts in LDS; returns total.
+__device__ int build_split_prefix(const DecodeArgs& a, int* prefix) {
+  const int n = a.n_rows;
+  __shared__ int wave_totals[kWaves];
+  const int per = (n + blockDim.x - 1) / blockDim.x;
+  const int lo = min(n, static_cast<int>(threadIdx.x) * per);
+  const int hi = min(n, lo + per);
+  int local = 0;
+  for (int r = lo; r < hi; ++r) {
+    int sl, ns;
+    split_plan(row_length(a, r), &sl, &ns);
+    local += ns;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wave_totals[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_totals[w];
+  int run = base + incl - local;
+  for (int r = lo; r < hi; ++r) {
+    prefix[r] = run;
+    int sl, ns;
+    split_plan(row_length(a, r), &sl, &ns);
+    run += ns;
+  }
+  int total = 0;
+  for (int w = 0; w < kWaves; ++w) total += wave_totals[w];
+  if (threadIdx.x == 0) prefix[n] = total;
+  __syncthreads();
+  return total;
+}
+
+// Largest r in [0, n) with prefix[r] <= x (prefix non-decreasing, x < prefix[n]).
+__device__ __forceinline__ int find_row(const int* prefix, int n, int x) {
+  int lo = 0, hi = n;  // invariant: prefix[lo] <= x < prefix[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (prefix[mid] <= x) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+template <typename T, int D, int G, int P, int TILE>
+__global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  using PK = Packet<T>;
+  constexpr int EPL = PK::N;      // elements of one token a lane owns
+  constexpr int LPT = D / EPL;    // lanes per token
+  constexpr int TPI = 64 / LPT;   // tokens per load instruction
+  constexpr int IPP = P / TPI;    // load instructions per page
+  constexpr int PPT = TILE / P;   // pages per tile
+  constexpr int NI = TILE / TPI;  // load instructions per tile (per tensor)
+  static_assert(D % EPL == 0 && 64 % LPT == 0 && LPT >= 1, "head_dim must map onto whole lanes");
+  static_assert(P % TPI == 0 && TILE % P == 0 && kSplitAlign % TILE == 0, "tile geometry");
+
+  extern __shared__ int prefix[];
+  const int total_splits = build_split_prefix(a, prefix);
+  const int total = total_splits * a.hkv;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int g = lane / LPT;
+  const int s = lane % LPT;
+  const uint32_t lane_dim = static_cast<uint32_t>(s * EPL);
+
+  for (int item = blockIdx.x * kWaves + wave; item < total; item += gridDim.x * kWaves) {
+    const int qi = item / a.hkv;
+    const int h = item - qi * a.hkv;
+    const int r = uniform(find_row(prefix, a.n_rows, qi));
+    const int sp = uniform(qi - prefix[r]);
+    const int len = uniform(row_length(a, r));
+    int split_len, ns;
+    split_plan(len, &split_len, &ns);
+    const int t_begin = sp * split_len;
+    const int t_end = min(len, t_begin + split_len);
+    const int last = t_end - 1;
+    const int first_page = t_begin / P;
+    const int last_rel_page = last / P - first_page;
+
+    // q for the G query heads of this kv head, pre-scaled into log2 units.
+    float qv[G][EPL];
+    {
+      const T* qrow = static_cast<const T*>(a.q) + r * a.q_row + static_cast<int64_t>(h) * G * a.q_head + lane_dim;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const u32x4 p = *reinterpret_cast<const u32x4*>(qrow + j * a.q_head);
+        PK::unpack(p, qv[j]);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) qv[j][e] *= a.qscale;
+      }
+    }
+
+    float m[G], l[G], acc[G][EPL];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      m[j] = -INFINITY;
+      l[j] = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[j][e] = 0.f;
+    }
+
+    const int32_t* trow = a.tables + r * a.table_stride;
+    const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.kv_head;
+    const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.kv_head;
+    const uint32_t tok_stride = static_cast<uint32_t>(a.kv_token);
+
+    // The split's table entries, 64 pages per chunk, one per lane; pages are
+    // picked out with readlane so every K/V load has a scalar page base.
+    int table_chunk = -1;
+    int table_entry = 0;
+    for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
+      const int rel0 = (t0 - t_begin) / P;
+      if ((rel0 >> 6) != table_chunk) {
+        table_chunk = rel0 >> 6;
+        const int rel = table_chunk * 64 + lane;
+        table_entry = rel <= last_rel_page ? trow[first_page + rel] : 0;
+      }
+      u32x4 kp[NI], vp[NI];
+#pragma unroll
+      for (int pg = 0; pg < PPT; ++pg) {
+        const int rel = min(rel0 + pg, last_rel_page);
+        int64_t blk = __builtin_amdgcn_readlane(table_entry, rel & 63);
+        blk = (blk < 0 || blk >= a.num_blocks) ? 0 : blk;
+        const T* kpage = kbase + blk * a.kv_block;
+        const T* vpage = vbase + blk * a.kv_block;
+#pragma unroll
+        for (int i = 0; i < IPP; ++i) {
+          const int tok = min(t0 + pg * P + i * TPI + g, last);
+          const uint32_t off = static_cast<uint32_t>(tok & (P - 1)) * tok_stride + lane_dim;
+          kp[pg * IPP + i] = *reinterpret_cast<const u32x4*>(kpage + off);
+          vp[pg * IPP + i] = *reinterpret_cast<const u32x4*>(vpage + off);
+        }
+      }
+
+      float sc[G][NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float x[EPL];
+        PK::unpack(kp[i], x);
+        const bool valid = t0 + i * TPI + g <= last;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          float dot = 0.f;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) dot = fmaf(qv[j][e], x[e], dot);
+          dot = group_sum<LPT>(dot);
+          sc[j][i] = valid ? dot : -INFINITY;
+        }
+      }
+
+      float p[G][NI];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        float tmax = sc[j][0];
+#pragma unroll
+        for (int i = 1; i < NI; ++i) tmax = fmaxf(tmax, sc[j][i]);
+        const float mn = fmaxf(m[j], tmax);
+        const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m[j] - mn);
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const bool valid = t0 + i * TPI + g <= last;
+          p[j][i] = valid ? fast_exp2(sc[j][i] - mn) : 0.f;
+          psum += p[j][i];
+        }
+        l[j] = l[j] * corr + psum;
+        m[j] = mn;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[j][e] *= corr;
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float y[EPL];
+        PK::unpack(vp[i], y);
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[j][e] = fmaf(p[j][i], y[e], acc[j][e]);
+      }
+    }
+
+    // Merge the token groups (lanes that share s).
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float M = strided_max<LPT>(m[j]);
+      const float f = (m[j] == -INFINITY) ? 0.f : fast_exp2(m[j] - M);
+      l[j] = strided_sum<LPT>(l[j] * f);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[j][e] = strided_sum<LPT>(acc[j][e] * f);
+      m[j] = M;
+    }
+
+    if (ns == 1) {
+      if (g == 0) {
+        T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h) * G * a.o_head + lane_dim;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          float o[EPL];
+          const float inv = 1.f / l[j];
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) o[e] = acc[j][e] * inv;
+          *reinterpret_cast<u32x4*>(orow + j * a.o_head) = PK::pack(o);
+        }
+      }
+    } else {
+      const int64_t slot = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits + sp;
+      if (g == 0) {
+        float* dst = a.ws_acc + slot * G * D + lane_dim;
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+          for (int e = 0; e < EPL; e += 4) {
+            u32x4 w;
+            w[0] = __float_as_uint(acc[j][e]);
+            w[1] = __float_as_uint(acc[j][e + 1]);
+            w[2] = __float_as_uint(acc[j][e + 2]);
+            w[3] = __float_as_uint(acc[j][e + 3]);
+            *reinterpret_cast<u32x4*>(dst + j * D + e) = w;
+          }
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) a.ws_ml[slot * G + j] = make_float2(m[j], l[j]);
+      }
+    }
+  }
+}
+
+// Merge kernel: one wavefront per (row, kv_head).  Zeroes empty rows and
+// merges multi-split partials in split order; single-split rows are done.
+template <typename T>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
+  const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (item >= a.n_rows * a.hkv) return;
+  const int lane = threadIdx.x & 63;
+  const int r = item / a.hkv;
+  const int h = item - r * a.hkv;
+  int split_len, ns;
+  split_plan(row_length(a, r), &split_len, &ns);
+  if (ns == 1) return;
+  const int G = a.hq / a.hkv;
+  const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
+  for (int j = 0; j < G; ++j) {
+    T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
+    if (ns == 0) {
+      for (int d = lane; d < a.d; d += 64) store_elem(orow + d * a.o_dim, 0.f);
+      continue;
+    }
+    float M = -INFINITY;
+    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, a.ws_ml[(slot0 + sp) * G + j].x);
+    float L = 0.f;
+    for (int sp = 0; sp < ns; ++sp) {
+      const float2 ml = a.ws_ml[(slot0 + sp) * G + j];
+      L += ml.y * fast_exp2(ml.x - M);
+    }
+    const float inv = 1.f / L;
+    for (int d = lane; d < a.d; d += 64) {
+      float acc = 0.f;
+      for (int sp = 0; sp < ns; ++sp) {
+        const float w = fast_exp2(a.ws_ml[(slot0 + sp) * G + j].x - M);
+        acc = fmaf(a.ws_acc[((slot0 + sp) * G + j) * a.d + d], w, acc);
+      }
+      store_elem(orow + d * a.o_dim, acc * inv);
+    }
+  }
+}
+
+// Generic kernel for shapes the tiled kernel does not cover (odd head_dim,
+// strided dims, any page size or group size): one wavefront per (row, q head),
+// tokens in order, same exp2-domain online softmax.  Correctness path only.
+constexpr int kGenericMaxPerLane = 8;  // head_dim <= 512
+
+template <typename T>
+__global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) {
+  const int r = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int G = a.hq / a.hkv;
+  const int h = hq / G;
+  const int len = row_length(a, r);
+  T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(hq) * a.o_head;
+  if (len <= 0) {
+    for (int d = lane; d < a.d; d += 64) store_elem(orow + d * a.o_dim, 0.f);
+    return;
+  }
+  const T* qrow = static_cast<const T*>(a.q) + r * a.q_row + static_cast<int64_t>(hq) * a.q_head;
+  float qv[kGenericMaxPerLane], acc[kGenericMaxPerLane];
+#pragma unroll
+  for (int c = 0; c < kGenericMaxPerLane; ++c) {
+    const int d = lane + 64 * c;
+    qv[c] = d < a.d ? load_elem(qrow + d * a.q_dim) * a.qscale : 0.f;
+    acc[c] = 0.f;
+  }
+  const int32_t* trow = a.tables + r * a.table_stride;
+  float m = -INFINITY, l = 0.f;
+  for (int t = 0; t < len; ++t) {
+    int64_t blk = trow[t / a.page];
+    blk = (blk < 0 || blk >= a.num_blocks) ? 0 : blk;
+    const int64_t base = blk * a.kv_block + static_cast<int64_t>(t % a.page) * a.kv_token +
+                         static_cast<int64_t>(h) * a.kv_head;
+    const T* kt = static_cast<const T*>(a.k) + base;
+    const T* vt = static_cast<const T*>(a.v) + base;
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < kGenericMaxPerLane; ++c) {
+      const int d = lane + 64 * c;
+      if (d < a.d) dot = fmaf(qv[c], load_elem(kt + d * a.kv_dim), dot);
+    }
+    dot = group_sum<64>(dot);
+    const float mn = fmaxf(m, dot);
+    const float corr = fast_exp2(m - mn);
+    const float p = fast_exp2(dot - mn);
+    l = l * corr + p;
+#pragma unroll
+    for (int c = 0; c < kGenericMaxPerLane; ++c) {
+      const int d = lane + 64 * c;
+      const float vv = d < a.d ? load_elem(vt + d * a.kv_dim) : 0.f;
+      acc[c] = fmaf(p, vv, acc[c] * corr);
+    }
+    m = mn;
+  }
+  const float inv = 1.f / l;
+#pragma unroll
+  for (int c = 0; c < kGenericMaxPerLane; ++c) {
+    const int d = lane + 64 * c;
+    if (d < a.d) store_elem(orow + d * a.o_dim, acc[c] * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+using DecodeKernel = void (*)(DecodeArgs);
+
+template <typename T, int D>
+DecodeKernel pick_group(int G) {
+  switch (G) {
+    case 1: return paged_decode_kernel<T, D, 1, 16, 32>;
+    case 2: return paged_decode_kernel<T, D, 2, 16, 32>;
+    case 4: return paged_decode_kernel<T, D, 4, 16, 32>;
+    case 8: return paged_decode_kernel<T, D, 8, 16, 32>;
+    default: return nullptr;
+  }
+}
+
+template <typename T>
+DecodeKernel pick_tiled(int d, int G);
+template <>
+DecodeKernel pick_tiled<bf16>(int d, int G) {
+  switch (d) {
+    case 64: return pick_group<bf16, 64>(G);
+    case 128: return pick_group<bf16, 128>(G);
+    case 256: return pick_group<bf16, 256>(G);
+    default: return nullptr;
+  }
+}
+template <>
+DecodeKernel pick_tiled<f16>(int d, int G) {
+  switch (d) {
+    case 64: return pick_group<f16, 64>(G);
+    case 128: return pick_group<f16, 128>(G);
+    case 256: return pick_group<f16, 256>(G);
+    default: return nullptr;
+  }
+}
+template <>
+DecodeKernel pick_tiled<float>(int d, int G) {
+  switch (d) {
+    case 64: return pick_group<float, 64>(G);
+    case 128: return pick_group<float, 128>(G);
+    default: return nullptr;
+  }
+}
+
+bool stride16(int64_t stride, int esize) { return (stride * esize) % 16 == 0; }
+
+template <typename T>
+int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
+  const int esize = sizeof(T);
+  const int G = a.hq / a.hkv;
+  DecodeKernel tiled = nullptr;
+  const bool layout_ok = a.page == 16 && a.q_dim == 1 && a.o_dim == 1 && a.kv_dim == 1 && aligned16(a.q) &&
+                         aligned16(a.out) && aligned16(a.k) && aligned16(a.v) && stride16(a.q_row, esize) &&
+                         stride16(a.q_head, esize) && stride16(a.o_row, esize) && stride16(a.o_head, esize) &&
+                         stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
+                         a.kv_token * a.page < (int64_t(1) << 31);
+  if (layout_ok) tiled = pick_tiled<T>(a.d, G);
+  if (!tiled) {
+    if (a.d > 64 * kGenericMaxPerLane) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: head_dim > 512");
+    if (a.hq > 65535) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: too many query heads");
+    hipLaunchKernelGGL(paged_decode_generic_kernel<T>, dim3(a.n_rows, a.hq), dim3(64), 0, stream, a);
+    return check_launch("rlt_paged_decode(generic)");
+  }
+  const int64_t max_tokens = max_table_width * a.page;
+  const int64_t splits_cap = std::min<int64_t>(kMaxSplits, (max_tokens + kSplitTokens - 1) / kSplitTokens);
+  const int64_t items = static_cast<int64_t>(a.n_rows) * a.hkv * std::max<int64_t>(splits_cap, 1);
+  const int grid = static_cast<int>(std::min<int64_t>(kMaxGrid, (items + kWaves - 1) / kWaves));
+  const size_t lds = static_cast<size_t>(a.n_rows + 1) * sizeof(int);
+  hipLaunchKernelGGL(tiled, dim3(grid), dim3(64 * kWaves), lds, stream, a);
+  if (int rc = check_launch("rlt_paged_decode")) return rc;
+  const int merge_grid = (a.n_rows * a.hkv + kWaves - 1) / kWaves;
+  hipLaunchKernelGGL(paged_decode_merge_kernel<T>, dim3(merge_grid), dim3(64 * kWaves), 0, stream, a);
+  return check_launch("rlt_paged_decode(merge)");
+}
+
+int64_t workspace_bytes_for(int64_t rows, int64_t hq, int64_t hkv, int64_t d) {
+  if (rows <= 0 || hq <= 0 || hkv <= 0 || d <= 0 || hq % hkv) return 0;
+  rows = std::min<int64_t>(rows, kMaxRowsPerLaunch);
+  const int64_t slots = rows * hkv * kMaxSplits * (hq / hkv);
+  const int64_t acc = slots * d * static_cast<int64_t>(sizeof(float));
+  const int64_t ml = slots * static_cast<int64_t>(sizeof(float2));
+  return (acc + 255) / 256 * 256 + ml;
+}
+
+}  // namespace
+}  // namespace rlt
+
+using namespace rlt;
+
+extern "C" int64_t rlt_paged_decode_workspace_bytes(int64_t n_rows, int64_t num_q_heads, int64_t num_kv_heads,
+                                                    int64_t head_dim) {
+  return workspace_bytes_for(n_rows, num_q_heads, num_kv_heads, head_dim);
+}
+
+extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
+                                const void* value_cache, const int64_t* kv_strides, const int32_t* block_tables,
+                                int64_t table_stride, int64_t max_table_width, const int32_t* context_lengths,
+                                void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
+                                int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks,
+                                float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int esize = dtype_size(dtype);
+  if (!esize) return fail(RLT_EINVAL, "rlt_paged_decode: unknown dtype %d", dtype);
+  if (n_rows < 0) return fail(RLT_EINVAL, "rlt_paged_decode: n_rows is negative");
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(RLT_EINVAL, "rlt_paged_decode: query heads must be a positive multiple of KV heads");
+  if (head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
+    return fail(RLT_EINVAL, "rlt_paged_decode: head_dim, page_size and num_blocks must be positive");
+  if (max_table_width < 0 || table_stride < 0) return fail(RLT_EINVAL, "rlt_paged_decode: bad table shape");
+  if (n_rows == 0) return RLT_OK;
+  if (!q || !key_cache || !value_cache || !block_tables || !context_lengths || !out || !q_strides || !kv_strides ||
+      !out_strides)
+    return fail(RLT_EINVAL, "rlt_paged_decode: NULL pointer argument");
+  if (num_q_heads > 4096 || head_dim > 4096 || page_size > (1 << 20))
+    return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: shape too large");
+  const int64_t need = workspace_bytes_for(n_rows, num_q_heads, num_kv_heads, head_dim);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(RLT_EWORKSPACE, "rlt_paged_decode: workspace of %lld bytes < required %lld",
+                (long long)workspace_bytes, (long long)need);
+  if (!aligned16(workspace)) return fail(RLT_EINVAL, "rlt_paged_decode: workspace must be 16-byte aligned");
+
+  DecodeArgs a{};
+  a.q_row = q_strides[0];
+  a.q_head = q_strides[1];
+  a.q_dim = q_strides[2];
+  a.k = key_cache;
+  a.v = value_cache;
+  a.kv_block = kv_strides[0];
+  a.kv_token = kv_strides[1];
+  a.kv_head = kv_strides[2];
+  a.kv_dim = kv_strides[3];
+  a.table_stride = table_stride;
+  a.o_row = out_strides[0];
+  a.o_head = out_strides[1];
+  a.o_dim = out_strides[2];
+  a.ws_acc = static_cast<float*>(workspace);
+  const int64_t rows_cap = std::min<int64_t>(n_rows, kMaxRowsPerLaunch);
+  const int64_t acc_bytes = rows_cap * num_kv_heads * kMaxSplits * (num_q_heads / num_kv_heads) * head_dim * 4;
+  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + (acc_bytes + 255) / 256 * 256);
+  a.hkv = static_cast<int>(num_kv_heads);
+  a.hq = static_cast<int>(num_q_heads);
+  a.d = static_cast<int>(head_dim);
+  a.page = static_cast<int>(page_size);
+  a.num_blocks = num_blocks;
+  a.max_len = max_table_width * page_size;
+  a.qscale = scale * kLog2e;
+  hipStream_t s = as_stream(stream);
+  for (int64_t r0 = 0; r0 < n_rows; r0 += kMaxRowsPerLaunch) {
+    const int64_t rows = std::min<int64_t>(kMaxRowsPerLaunch, n_rows - r0);
+    a.q = static_cast<const char*>(q) + r0 * q_strides[0] * esize;
+    a.out = static_cast<char*>(out) + r0 * out_strides[0] * esize;
+    a.tables = block_tables + r0 * table_stride;
+    a.lens = context_lengths + r0;
+    a.n_rows = static_cast<int>(rows);
+    int rc = RLT_OK;
+    switch (dtype) {
+      case RLT_BFLOAT16: rc = launch_decode<bf16>(a, max_table_width, s); break;
+      case RLT_FLOAT16: rc = launch_decode<f16>(a, max_table_width, s); break;
+      default: rc = launch_decode<float>(a, max_table_width, s); break;
+    }
+    if (rc) return rc;
+  }
+  return RLT_OK;
+}

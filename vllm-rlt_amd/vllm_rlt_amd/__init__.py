@@ -1,0 +1,11 @@
+"""MI355X-native (gfx950) depth-aware paged-KV hot path for looped LMs.
+
+A drop-in "hip" backend for vllm_rlt's KV-cache manager and attention-backend
+interfaces, backed by hand-written HIP kernels in librlt_kv.so (C ABI in
+include/rlt_kv.h).
+"""
+
+from . import ops
+from .paged_attention import HipPagedAttention, hip_paged_attention
+
+__all__ = ["HipPagedAttention", "hip_paged_attention", "ops"]

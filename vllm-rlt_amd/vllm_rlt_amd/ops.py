@@ -1,0 +1,460 @@
+"""Tensor-level entry points over the librlt_kv C ABI.
+
+Each function validates shapes, dtypes and devices on the host (raising
+ValueError, as the reference's callers expect) and then enqueues the HIP
+kernel on the current stream of the tensors' device.  Nothing here computes on
+the CPU and nothing falls back to another implementation.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native
+from ._native import check, dtype_code, int64_array, stream_handle
+
+
+def _require_rocm(*tensors: torch.Tensor) -> torch.device:
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise ValueError("the hip backend requires a ROCm device")
+    for t in tensors[1:]:
+        if t.device != device:
+            raise ValueError("all tensors must be on the same ROCm device")
+    return device
+
+
+def _require_int(t: torch.Tensor, dtype: torch.dtype, name: str, ndim: int = 1) -> None:
+    if t.dtype != dtype or t.ndim != ndim:
+        raise ValueError(f"{name} must be a {ndim}-D {dtype} tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def kv_append(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    layer: int,
+    write_blocks: torch.Tensor,
+    write_offsets: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    n_rows: int | None = None,
+) -> None:
+    """key_cache[write_blocks[i], layer, write_offsets[i]] = k[i] (and V) for i < n_rows.
+
+    Mirrors the index_put pair of vllm_rlt/core/kv_cache_manager.py:531-532.
+    """
+    device = _require_rocm(key_cache, value_cache, write_blocks, write_offsets, k, v)
+    if key_cache.shape != value_cache.shape or key_cache.stride() != value_cache.stride():
+        raise ValueError("key_cache and value_cache must share shape and strides")
+    if key_cache.ndim != 5:
+        raise ValueError("caches must be [blocks, layers, page, kv_heads, head_dim]")
+    nb, nl, page, hkv, d = key_cache.shape
+    for t, name in ((k, "k"), (v, "v")):
+        if t.ndim != 3 or t.shape[1:] != (hkv, d):
+            raise ValueError(f"{name} must have shape [batch, {hkv}, {d}]")
+        if t.dtype != key_cache.dtype:
+            raise ValueError(f"{name} must use dtype {key_cache.dtype}")
+    _require_int(write_blocks, torch.int64, "write_blocks")
+    _require_int(write_offsets, torch.int64, "write_offsets")
+    n = len(write_blocks) if n_rows is None else n_rows
+    if n > min(len(write_blocks), len(write_offsets), k.shape[0], v.shape[0]):
+        raise ValueError("n_rows exceeds the provided rows")
+    lib = _native.load()
+    rc = lib.rlt_kv_append(
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        k.data_ptr(),
+        int64_array(k.stride()),
+        v.data_ptr(),
+        int64_array(v.stride()),
+        write_blocks.data_ptr(),
+        write_offsets.data_ptr(),
+        n,
+        layer,
+        nl,
+        nb,
+        page,
+        hkv,
+        d,
+        dtype_code(key_cache.dtype),
+        stream_handle(device),
+    )
+    check(rc, "rlt_kv_append")
+
+
+def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))
+
+
+def paged_decode(
+    q: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lengths: torch.Tensor,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Paged decode attention over layer-slice caches [blocks, page, kv_heads, head_dim].
+
+    Same contract as torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36):
+    returns a new tensor like q unless out is given.
+    """
+    device = _require_rocm(q, key_cache, value_cache, block_tables, context_lengths)
+    if q.ndim != 3 or key_cache.ndim != 4:
+        raise ValueError("q must be [rows, heads, head_dim] and caches [blocks, page, kv_heads, head_dim]")
+    if key_cache.shape != value_cache.shape or key_cache.stride() != value_cache.stride():
+        raise ValueError("key_cache and value_cache must share shape and strides")
+    nb, page, hkv, d = key_cache.shape
+    rows, hq, qd = q.shape
+    if qd != d:
+        raise ValueError(f"q head_dim {qd} does not match cache head_dim {d}")
+    if hq == 0 or hq % hkv:
+        raise ValueError("query heads must be a positive multiple of KV heads")
+    if q.dtype != key_cache.dtype or value_cache.dtype != key_cache.dtype:
+        raise ValueError("q, key_cache and value_cache must share a dtype")
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be int32 [rows, width] with contiguous rows")
+    if block_tables.shape[0] != rows or context_lengths.shape != (rows,):
+        raise ValueError("block_tables and context_lengths must have one entry per row")
+    _require_int(context_lengths, torch.int32, "context_lengths")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != device:
+        raise ValueError("out must match q")
+    if rows == 0:
+        return out
+    need = decode_workspace_bytes(rows, hq, hkv, d)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
+        raise ValueError(f"workspace must hold {need} bytes on {device}")
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    rc = _native.load().rlt_paged_decode(
+        q.data_ptr(),
+        int64_array(q.stride()),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        block_tables.data_ptr(),
+        block_tables.stride(0),
+        block_tables.shape[1],
+        context_lengths.data_ptr(),
+        out.data_ptr(),
+        int64_array(out.stride()),
+        rows,
+        hq,
+        hkv,
+        d,
+        page,
+        nb,
+        scale,
+        dtype_code(q.dtype),
+        workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(),
+        stream_handle(device),
+    )
+    check(rc, "rlt_paged_decode")
+    return out
+
+
+def paged_prefill(
+    q: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lengths: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    max_seqlen_q: int,
+    out: torch.Tensor | None = None,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Packed bottom-right-causal prefill (FlashPagedAttention.prefill, flash_attention.py:66-96)."""
+    device = _require_rocm(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q)
+    if q.ndim != 3 or key_cache.ndim != 4:
+        raise ValueError("q must be [tokens, heads, head_dim] and caches [blocks, page, kv_heads, head_dim]")
+    if key_cache.shape != value_cache.shape or key_cache.stride() != value_cache.stride():
+        raise ValueError("key_cache and value_cache must share shape and strides")
+    nb, page, hkv, d = key_cache.shape
+    total, hq, qd = q.shape
+    if qd != d or hq == 0 or hq % hkv:
+        raise ValueError("q must have head_dim matching the cache and a positive multiple of KV heads")
+    if q.dtype != key_cache.dtype:
+        raise ValueError("q and the caches must share a dtype")
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be int32 [sequences, width] with contiguous rows")
+    _require_int(context_lengths, torch.int32, "context_lengths")
+    _require_int(cu_seqlens_q, torch.int32, "cu_seqlens_q")
+    nseq = block_tables.shape[0]
+    if context_lengths.shape != (nseq,) or cu_seqlens_q.shape != (nseq + 1,):
+        raise ValueError("context_lengths and cu_seqlens_q must describe one entry per sequence")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != device:
+        raise ValueError("out must match q")
+    if total == 0 or nseq == 0:
+        return out
+    width = block_tables.shape[1]
+    lib = _native.load()
+    need = int(lib.rlt_paged_prefill_workspace_bytes(total, nseq, width, hq, hkv, d))
+    workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    rc = lib.rlt_paged_prefill(
+        q.data_ptr(),
+        int64_array(q.stride()),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        block_tables.data_ptr(),
+        block_tables.stride(0),
+        width,
+        context_lengths.data_ptr(),
+        cu_seqlens_q.data_ptr(),
+        nseq,
+        total,
+        max_seqlen_q,
+        out.data_ptr(),
+        int64_array(out.stride()),
+        hq,
+        hkv,
+        d,
+        page,
+        nb,
+        scale,
+        dtype_code(q.dtype),
+        workspace.data_ptr(),
+        need,
+        stream_handle(device),
+    )
+    check(rc, "rlt_paged_prefill")
+    return out
+
+
+def _pool_dims(key_cache: torch.Tensor, value_cache: torch.Tensor):
+    if key_cache.ndim != 5 or key_cache.shape != value_cache.shape or key_cache.stride() != value_cache.stride():
+        raise ValueError("caches must be matching [blocks, layers, page, kv_heads, head_dim] tensors")
+    return key_cache.shape
+
+
+def kv_copy_token(
+    key_cache: torch.Tensor, value_cache: torch.Tensor, src_block: int, dst_blocks, offset: int
+) -> None:
+    """cache[dst, :, offset] = cache[src_block, :, offset] for every dst (all layers, K and V).
+
+    Mirrors the exit copies of finalize_token, vllm_rlt/core/kv_cache_manager.py:601-611.
+    """
+    device = _require_rocm(key_cache, value_cache)
+    nb, nl, page, hkv, d = _pool_dims(key_cache, value_cache)
+    dst = list(dst_blocks)
+    rc = _native.load().rlt_kv_copy_token(
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        src_block,
+        int64_array(dst or [0]),
+        len(dst),
+        offset,
+        nl,
+        nb,
+        page,
+        hkv,
+        d,
+        dtype_code(key_cache.dtype),
+        stream_handle(device),
+    )
+    check(rc, "rlt_kv_copy_token")
+
+
+def kv_finalize(
+    descriptors: torch.Tensor,
+    tables: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    max_loops: int,
+    count: int | None = None,
+) -> None:
+    """Batched LAST-EXITED exit copies (finalize_kernel, vllm_rlt/kernels/routing.py:80-109).
+
+    descriptors: int64 [n, 3] of (slot, exit depth, position), device or pinned host.
+    tables: int32 [slots, planes, width] device-resident page tables.
+    """
+    device = _require_rocm(key_cache, value_cache, tables)
+    nb, nl, page, hkv, d = _pool_dims(key_cache, value_cache)
+    if descriptors.dtype != torch.int64 or descriptors.ndim != 2 or descriptors.shape[1] != 3:
+        raise ValueError("descriptors must be int64 [n, 3]")
+    if not descriptors.is_contiguous():
+        raise ValueError("descriptors must be contiguous")
+    if descriptors.device.type == "cpu" and not descriptors.is_pinned():
+        raise ValueError("host descriptors must be pinned")
+    if tables.dtype != torch.int32 or tables.ndim != 3 or not tables.is_contiguous():
+        raise ValueError("tables must be contiguous int32 [slots, planes, width]")
+    n = descriptors.shape[0] if count is None else count
+    rc = _native.load().rlt_kv_finalize(
+        descriptors.data_ptr(),
+        n,
+        tables.data_ptr(),
+        tables.shape[2],
+        tables.shape[1],
+        tables.shape[0],
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        nl,
+        nb,
+        hkv,
+        d,
+        page,
+        max_loops,
+        dtype_code(key_cache.dtype),
+        stream_handle(device),
+    )
+    check(rc, "rlt_kv_finalize")
+
+
+def kv_gather(
+    key_cache: torch.Tensor, value_cache: torch.Tensor, layer: int, table: torch.Tensor, length: int
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Ordered [length, kv_heads, head_dim] K and V of one table (read(), kv_cache_manager.py:616-637)."""
+    device = _require_rocm(key_cache, value_cache, table)
+    nb, nl, page, hkv, d = _pool_dims(key_cache, value_cache)
+    _require_int(table, torch.int32, "table")
+    if length < 0 or (length + page - 1) // page > table.numel():
+        raise ValueError("length exceeds the table")
+    out_k = torch.empty((length, hkv, d), dtype=key_cache.dtype, device=device)
+    out_v = torch.empty_like(out_k)
+    if length == 0:
+        return out_k, out_v
+    rc = _native.load().rlt_kv_gather(
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        layer,
+        table.data_ptr(),
+        length,
+        out_k.data_ptr(),
+        out_v.data_ptr(),
+        nl,
+        nb,
+        page,
+        hkv,
+        d,
+        dtype_code(key_cache.dtype),
+        stream_handle(device),
+    )
+    check(rc, "rlt_kv_gather")
+    return out_k, out_v
+
+
+def build_decode_metadata(
+    descriptors: torch.Tensor,
+    count: int,
+    size: int,
+    tables: torch.Tensor,
+    page_size: int,
+    slots: torch.Tensor,
+    positions: torch.Tensor,
+    lengths: torch.Tensor,
+    blocks: torch.Tensor,
+    offsets: torch.Tensor,
+    out_tables: torch.Tensor,
+    out_width: int,
+) -> None:
+    """Per-row routing metadata on the device (metadata_kernel, vllm_rlt/kernels/routing.py:8-41)."""
+    device = _require_rocm(tables, slots, positions, lengths, blocks, offsets, out_tables)
+    if tables.dtype != torch.int32 or tables.ndim != 3 or not tables.is_contiguous():
+        raise ValueError("tables must be contiguous int32 [slots, planes, width]")
+    if descriptors.dtype != torch.int64 or descriptors.ndim != 2 or descriptors.shape[1] != 3:
+        raise ValueError("descriptors must be int64 [n, 3]")
+    if descriptors.device.type == "cpu" and not descriptors.is_pinned():
+        raise ValueError("host descriptors must be pinned")
+    if out_tables.dtype != torch.int32 or out_tables.ndim != 2 or out_tables.stride(1) != 1:
+        raise ValueError("out_tables must be int32 [rows, width] with contiguous rows")
+    for t, dt, name in (
+        (slots, torch.int64, "slots"),
+        (positions, torch.int64, "positions"),
+        (lengths, torch.int32, "lengths"),
+        (blocks, torch.int64, "blocks"),
+        (offsets, torch.int64, "offsets"),
+    ):
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous {dt}")
+    if min(slots.numel(), positions.numel(), lengths.numel(), out_tables.shape[0]) < size:
+        raise ValueError("output buffers are smaller than size")
+    if min(blocks.numel(), offsets.numel(), descriptors.shape[0]) < count:
+        raise ValueError("descriptor/address buffers are smaller than count")
+    rc = _native.load().rlt_build_decode_metadata(
+        descriptors.data_ptr(),
+        count,
+        size,
+        tables.data_ptr(),
+        tables.shape[0],
+        tables.shape[2],
+        tables.shape[1],
+        page_size,
+        slots.data_ptr(),
+        positions.data_ptr(),
+        lengths.data_ptr(),
+        blocks.data_ptr(),
+        offsets.data_ptr(),
+        out_tables.data_ptr(),
+        out_tables.stride(0),
+        out_width,
+        stream_handle(device),
+    )
+    check(rc, "rlt_build_decode_metadata")
+
+
+def stage_prefill(source: torch.Tensor, target: torch.Tensor, target32: torch.Tensor, n: int) -> None:
+    """Copy n int64 values to int64 and int32 device buffers (stage_prefill, prefill_metadata.py:8-12)."""
+    device = _require_rocm(target, target32)
+    if source.dtype != torch.int64 or target.dtype != torch.int64 or target32.dtype != torch.int32:
+        raise ValueError("stage_prefill expects int64 source/target and int32 target32")
+    if source.device.type == "cpu" and not source.is_pinned():
+        raise ValueError("host source must be pinned")
+    if min(source.numel(), target.numel(), target32.numel()) < n:
+        raise ValueError("buffers are smaller than n")
+    check(
+        _native.load().rlt_stage_prefill(
+            source.data_ptr(), target.data_ptr(), target32.data_ptr(), n, stream_handle(device)
+        ),
+        "rlt_stage_prefill",
+    )
+
+
+def expand_prefill(
+    positions: torch.Tensor,
+    sequences: torch.Tensor,
+    tables: torch.Tensor,
+    page_size: int,
+    blocks: torch.Tensor,
+    offsets: torch.Tensor,
+    n: int,
+) -> None:
+    """Per-token write addresses of a packed prefill (expand_prefill, prefill_metadata.py:16-32)."""
+    device = _require_rocm(positions, sequences, tables, blocks, offsets)
+    if tables.dtype != torch.int32 or tables.ndim != 2 or not tables.is_contiguous():
+        raise ValueError("tables must be contiguous int32 [sequences, width]")
+    for t, name in ((positions, "positions"), (sequences, "sequences"), (blocks, "blocks"), (offsets, "offsets")):
+        if t.dtype != torch.int64 or t.numel() < n:
+            raise ValueError(f"{name} must be int64 with at least n entries")
+    check(
+        _native.load().rlt_expand_prefill(
+            positions.data_ptr(),
+            sequences.data_ptr(),
+            tables.data_ptr(),
+            tables.shape[0],
+            tables.shape[1],
+            page_size,
+            blocks.data_ptr(),
+            offsets.data_ptr(),
+            n,
+            stream_handle(device),
+        ),
+        "rlt_expand_prefill",
+    )
