@@ -1,0 +1,401 @@
+"""Paged decode attention + KV append on Ouro-1.4B-shaped synthetic data (one MI355X).
+
+Workload (default, "ouro-last-exited"): 24 layers x 4 loop depths (LAST-EXITED:
+one storage plane per depth), 16 query / 16 KV heads, head_dim 128, page 16,
+bf16.  Batch 64; request contexts uniform in [512, 4096]; every step each
+request sits at a depth drawn uniformly from {1..4} (planes 0..3), appends one
+token's K/V at that depth for all 24 layers and runs decode attention over the
+depth-resolved pages.  Block tables are random page permutations.
+
+One "loop-step" = one recurrent pass of the whole batch: the device-side
+routing metadata build, then 24 x (KV append + paged decode attention).
+Positions advance by one per step.  Inputs live in HBM before timing starts.
+
+Prints one JSON line (bench contract) with loop-steps/s as `value`, the
+step's algorithmic HBM GB/s, the decode launch's roofline (algorithmic bytes /
+HIP-event-timed duration), and the CPU oracle's throughput on a bounded
+sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _path in (REPO, REPO / "vllm-rlt_amd"):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+LAYERS, HQ, HKV, HEAD_DIM, PAGE, LOOPS = 24, 16, 16, 128, 16, 4
+
+WORKLOADS = {
+    "ouro-last-exited": dict(batch=64, ctx=(512, 4096), planes=LOOPS, depth_probs=None),
+    "ouro-shared": dict(batch=256, ctx=(1024, 8192), planes=1, depth_probs=(0.1, 0.2, 0.3, 0.4)),
+}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="ouro-last-exited")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--cpu-reps", type=int, default=3, help="timed repetitions of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-check", action="store_true", help="skip the pre-timing parity spot check")
+    p.add_argument(
+        "--calibrate-counters",
+        action="store_true",
+        help="only run one 1 GiB device-to-device copy (known-size kernel for scaling HBM counters)",
+    )
+    return p.parse_args()
+
+
+def calibrate_counters(device):
+    """One plain 1 GiB copy: rocprofv3 FETCH_SIZE / WRITE_SIZE of this dispatch give the counter scale."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": src.numel()}), flush=True)
+
+
+def profiled_traffic(workload):
+    """HBM bytes per decode launch recorded by the committed rocprofv3 --pmc summary, if any.
+
+    The summary carries a line `traffic_bytes_per_launch[<workload>] = <bytes>`
+    computed from FETCH_SIZE and WRITE_SIZE scaled by the calibration copy.
+    """
+    import re
+
+    pattern = re.compile(rf"traffic_bytes_per_launch\[{re.escape(workload)}\]\s*=\s*(\d+)")
+    for path in sorted((REPO / "profiles").glob("*.md")):
+        match = pattern.search(path.read_text())
+        if match:
+            return int(match.group(1))
+    return None
+
+
+class Workload:
+    """Device-resident pool, page tables, per-step descriptors and per-layer inputs."""
+
+    def __init__(self, name, total_steps, seed, device):
+        cfg = WORKLOADS[name]
+        self.name = name
+        self.batch = cfg["batch"]
+        self.planes = cfg["planes"]
+        self.device = device
+        g = torch.Generator().manual_seed(seed)
+        lo, hi = cfg["ctx"]
+        self.contexts = torch.randint(lo, hi + 1, (self.batch,), generator=g)
+        # Capacity for every position the run will touch.
+        capacity = self.contexts + total_steps
+        pages = (capacity + PAGE - 1) // PAGE
+        self.width = int(pages.max())
+        self.num_blocks = int(pages.sum()) * self.planes
+        perm = torch.randperm(self.num_blocks, generator=g)
+        tables = torch.zeros(self.batch, self.planes, self.width, dtype=torch.int32)
+        used = 0
+        for r in range(self.batch):
+            for plane in range(self.planes):
+                n = int(pages[r])
+                tables[r, plane, :n] = perm[used : used + n].to(torch.int32)
+                used += n
+        self.tables_host = tables
+        self.tables = tables.to(device)
+        # Per-step (slot, depth, position) descriptors.
+        if cfg["depth_probs"] is None:
+            depths = torch.randint(0, LOOPS, (total_steps, self.batch), generator=g)
+        else:
+            probs = torch.tensor(cfg["depth_probs"])
+            depths = torch.multinomial(probs, total_steps * self.batch, replacement=True, generator=g)
+            depths = depths.view(total_steps, self.batch)
+        steps = torch.arange(total_steps)[:, None]
+        desc = torch.stack(
+            [
+                torch.arange(self.batch).expand(total_steps, -1),
+                depths if self.planes > 1 else torch.zeros_like(depths),
+                self.contexts[None, :] + steps,
+            ],
+            dim=-1,
+        ).to(torch.int64)
+        self.depths = depths
+        self.descriptors = desc.to(device)  # [steps, batch, 3]
+        # Pool [blocks, layers, page, kv_heads, head_dim], filled with N(0,1) bf16.
+        shape = (self.num_blocks, LAYERS, PAGE, HKV, HEAD_DIM)
+        self.key_cache = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        self.value_cache = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        gen = torch.Generator(device=device).manual_seed(seed + 1)
+        for pool in (self.key_cache, self.value_cache):
+            flat = pool.view(-1)
+            chunk = 1 << 28
+            for start in range(0, flat.numel(), chunk):
+                flat[start : start + chunk].normal_(generator=gen)
+        # Per-layer synthetic projections (q, new k, new v).
+        self.q = torch.randn((LAYERS, self.batch, HQ, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        self.k_new = torch.randn((LAYERS, self.batch, HKV, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        self.v_new = torch.randn((LAYERS, self.batch, HKV, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        self.out = torch.empty_like(self.q)
+        # Routing outputs of the metadata build (one set, rebuilt every step).
+        n = self.batch
+        self.slots = torch.empty(n, dtype=torch.int64, device=device)
+        self.positions = torch.empty(n, dtype=torch.int64, device=device)
+        self.lengths = torch.empty(n, dtype=torch.int32, device=device)
+        self.blocks = torch.empty(n, dtype=torch.int64, device=device)
+        self.offsets = torch.empty(n, dtype=torch.int64, device=device)
+        self.row_tables = torch.zeros((n, self.width), dtype=torch.int32, device=device)
+        from vllm_rlt_amd import ops
+
+        self.workspace = torch.empty(
+            ops.decode_workspace_bytes(n, HQ, HKV, HEAD_DIM), dtype=torch.uint8, device=device
+        )
+
+    def lengths_at(self, step):
+        """Attention length of every row at a step (context incl. the appended token)."""
+        return (self.contexts + step + 1).tolist()
+
+    def pool_bytes(self):
+        return 2 * self.key_cache.numel() * self.key_cache.element_size()
+
+
+def build_metadata(w, step):
+    from vllm_rlt_amd import ops
+
+    ops.build_decode_metadata(
+        w.descriptors[step], w.batch, w.batch, w.tables, PAGE, w.slots, w.positions, w.lengths,
+        w.blocks, w.offsets, w.row_tables, w.width,
+    )
+
+
+def layer_step(w, layer):
+    from vllm_rlt_amd import ops
+
+    ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
+    ops.paged_decode(
+        w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
+        out=w.out[layer], workspace=w.workspace,
+    )
+
+
+def loop_step(w, step):
+    build_metadata(w, step)
+    for layer in range(LAYERS):
+        layer_step(w, layer)
+
+
+def step_bytes(lengths):
+    """Algorithmic HBM bytes of one loop-step (24 layer-steps) and of one decode launch."""
+    kv_token = 2 * HKV * HEAD_DIM * 2  # K+V of one token in one layer (8 KiB)
+    qo = 2 * HQ * HEAD_DIM * 2  # q read + out write
+    new_kv = 2 * HKV * HEAD_DIM * 2
+    decode = sum(kv_token * n + qo + 4 * math.ceil(n / PAGE) + 4 for n in lengths)
+    append = len(lengths) * (2 * new_kv + 16)  # read new k/v, write the page slots, block+offset
+    return LAYERS * (decode + append), decode
+
+
+def spot_check(w):
+    """Parity of the first step's layer 0 against the CPU oracle on a row sample (untimed)."""
+    from oracle.paged_attention import paged_attention_cpu
+
+    sample = [0, w.batch // 2, w.batch - 1]
+    torch.cuda.synchronize()
+    rows = torch.tensor(sample)
+    tables = w.row_tables[rows].cpu()
+    lengths = w.lengths[rows].cpu()
+    need = sorted({int(b) for r in range(len(sample)) for b in tables[r, : math.ceil(int(lengths[r]) / PAGE)]})
+    remap = {b: i for i, b in enumerate(need)}
+    idx = torch.tensor(need, device=w.device)
+    kc = w.key_cache[idx, 0].cpu()
+    vc = w.value_cache[idx, 0].cpu()
+    local = torch.full_like(tables, -1)
+    for r in range(len(sample)):
+        for c in range(math.ceil(int(lengths[r]) / PAGE)):
+            local[r, c] = remap[int(tables[r, c])]
+    expect = paged_attention_cpu(w.q[0][rows].cpu(), kc, vc, local, lengths)
+    got = w.out[0][rows].cpu()
+    err = (got.float() - expect.float()).abs().max().item()
+    if not torch.allclose(got.float(), expect.float(), atol=2e-2, rtol=1e-2):
+        raise SystemExit(f"parity spot check failed: max-abs error {err}")
+    return err
+
+
+def cpu_baseline(w, step, reps):
+    """The CPU oracle (op-for-op restatement of the reference CPU path) on one layer-step.
+
+    Sample: every row of the workload at `step`, one layer: index_put-style KV
+    append plus paged attention over a 1-layer host copy of exactly the pages
+    those rows reference.  loop-steps/s = 1 / (24 * median layer-step time).
+    """
+    from oracle import kv_ops
+    from oracle.paged_attention import paged_attention_cpu
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    torch.cuda.synchronize()
+    lengths = w.lengths.cpu()
+    tables = w.row_tables.cpu()
+    need = sorted({int(b) for r in range(w.batch) for b in tables[r, : math.ceil(int(lengths[r]) / PAGE)]})
+    remap = torch.full((w.num_blocks,), -1, dtype=torch.int64)
+    remap[torch.tensor(need)] = torch.arange(len(need))
+    idx = torch.tensor(need, device=w.device)
+    kc = w.key_cache[idx, 0:1].cpu()  # [used blocks, 1 layer, page, hkv, d]
+    vc = w.value_cache[idx, 0:1].cpu()
+    local = torch.where(tables >= 0, remap[tables.clamp_min(0).long()], -1).to(torch.int32)
+    blocks = remap[w.blocks.cpu()]
+    offsets = w.offsets.cpu()
+    q, k_new, v_new = w.q[0].cpu(), w.k_new[0].cpu(), w.v_new[0].cpu()
+    times = []
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        kv_ops.append(kc, vc, 0, blocks, offsets, k_new, v_new)
+        paged_attention_cpu(q, kc[:, 0], vc[:, 0], local, lengths)
+        times.append(time.perf_counter() - t0)
+    layer_s = statistics.median(times[1:])
+    return {
+        "value": 1.0 / (LAYERS * layer_s),
+        "unit": "loop-steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one layer-step (all {w.batch} rows, 1 layer, append + attention), median of {reps} "
+        f"after 1 warmup, extrapolated x{LAYERS} layers; {layer_s * 1e3:.1f} ms/layer-step; "
+        f"cpu={platform.processor() or platform.machine()}",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the decode path shards with no "
+            "cross-GPU exchange; see DESIGN.md for the multi-GPU layout)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a ROCm device")
+    from vllm_rlt_amd import _native
+
+    if not _native.LIBRARY_PATH.exists():
+        import __graft_entry__
+
+        __graft_entry__.build()
+    _native.load()
+
+    device = torch.device("cuda:0")
+    if args.calibrate_counters:
+        calibrate_counters(device)
+        return
+    total = args.warmup + args.steps
+    t_setup = time.perf_counter()
+    w = Workload(args.workload, total, args.seed, device)
+    torch.cuda.synchronize()
+    print(
+        f"[bench] workload {args.workload}: batch {w.batch}, planes {w.planes}, pool "
+        f"{w.pool_bytes() / 1e9:.1f} GB ({w.num_blocks} pages), setup {time.perf_counter() - t_setup:.1f}s",
+        file=sys.stderr,
+        flush=True,
+    )
+
+    # Warmup (also the parity spot check on step 0).
+    for step in range(args.warmup):
+        loop_step(w, step)
+        if step == 0 and not args.no_check:
+            err = spot_check(w)
+            print(f"[bench] parity spot check ok (max-abs {err:.3g})", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` loop-steps.
+    total_bytes = 0
+    decode_bytes = []
+    for step in range(args.warmup, total):
+        b, d = step_bytes(w.lengths_at(step))
+        total_bytes += b
+        decode_bytes.append(d)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for step in range(args.warmup, total):
+        loop_step(w, step)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    # Decode-launch timing with HIP events on the launch stream (separate pass,
+    # same steps): each event pair brackets one rlt_paged_decode call.
+    from vllm_rlt_amd import ops
+
+    stream = torch.cuda.current_stream(device)
+    pairs = []
+    for step in range(args.warmup, total):
+        build_metadata(w, step)
+        for layer in range(LAYERS):
+            ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            ops.paged_decode(
+                w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
+                out=w.out[layer], workspace=w.workspace,
+            )
+            end.record(stream)
+            pairs.append((start, end))
+    torch.cuda.synchronize()
+    decode_ms = statistics.fmean(s.elapsed_time(e) for s, e in pairs)
+    decode_avg_bytes = statistics.fmean(decode_bytes)
+    achieved = decode_avg_bytes / (decode_ms * 1e-3) / 1e9
+
+    steps_per_s = args.steps / elapsed
+    gbs = total_bytes / elapsed / 1e9
+    line = {
+        "metric": "paged decode attn+KV append: HBM GB/s (% peak), loop-steps/s at Ouro-1.4B",
+        "value": round(steps_per_s, 3),
+        "unit": "loop-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: Ouro-1.4B decode, 24 layers, {w.planes} KV plane(s), 16/16 heads, "
+            f"head_dim 128, page 16, batch {w.batch}, contexts U[{WORKLOADS[args.workload]['ctx'][0]},"
+            f"{WORKLOADS[args.workload]['ctx'][1]}], loop-step = metadata build + 24 x (KV append + decode)",
+            "global_batch": w.batch,
+            "seq_len": int(w.contexts.float().mean().item()),
+            "parallelism": "single-gpu",
+        },
+        "hbm_gb_per_s": round(gbs, 1),
+        "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "kernel": "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": profiled_traffic(args.workload),
+            "avg_launch_ms": round(decode_ms, 5),
+            "algorithmic_bytes_per_launch": int(decode_avg_bytes),
+        },
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(w, total - 1, args.cpu_reps)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

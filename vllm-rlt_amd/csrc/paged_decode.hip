@@ -27,7 +27,10 @@
 //
 // Multi-split rows write (max, sum, unnormalised acc) partials to the
 // workspace; a second kernel merges them in split order.  Single-split rows
-// write their output directly; empty rows are zeroed by the merge kernel.
+// write their output directly and an empty row is one item that writes zeros.
+// (Merging inside the split kernel, by the last split to finish, needs an
+// agent-scope release/acquire per split -- an L2 writeback and invalidate
+// across the 8 XCDs -- and measured 3x slower than the separate merge.)
 #include <algorithm>
 
 #include "common.hpp"
@@ -35,18 +38,33 @@
 namespace rlt {
 namespace {
 
+// Tuning constants (overridable at compile time for measurement builds).
+#ifndef RLT_DECODE_SPLIT_TOKENS
+#define RLT_DECODE_SPLIT_TOKENS 256
+#endif
+#ifndef RLT_DECODE_TILE
+#define RLT_DECODE_TILE 32
+#endif
+#ifndef RLT_DECODE_NT_LOADS
+#define RLT_DECODE_NT_LOADS 1
+#endif
+
 constexpr int kWaves = 4;
-constexpr int kSplitTokens = 256;
+constexpr int kSplitTokens = RLT_DECODE_SPLIT_TOKENS;
+constexpr int kTile = RLT_DECODE_TILE;
 constexpr int kMaxSplits = 64;
 constexpr int kSplitAlign = 64;
 constexpr int kMaxRowsPerLaunch = 8192;
-constexpr int kMaxGrid = 4096;
+#ifndef RLT_DECODE_MAX_GRID
+#define RLT_DECODE_MAX_GRID 4096
+#endif
+constexpr int kMaxGrid = RLT_DECODE_MAX_GRID;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __host__ __device__ inline void split_plan(int len, int* split_len, int* nsplit) {
-  if (len <= 0) {
+  if (len <= 0) {  // one item that writes the all-zero row
     *split_len = kSplitTokens;
-    *nsplit = 0;
+    *nsplit = 1;
     return;
   }
   const int n = (len + kSplitTokens - 1) / kSplitTokens;
@@ -84,6 +102,15 @@ struct DecodeArgs {
 __device__ __forceinline__ int row_length(const DecodeArgs& a, int r) {
   const int64_t len = a.lens[r];
   return static_cast<int>(len < a.max_len ? len : a.max_len);
+}
+
+// K/V page reads: each byte is read once per launch.
+__device__ __forceinline__ u32x4 load_page(const u32x4* p) {
+#if RLT_DECODE_NT_LOADS
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
 }
 
 // Builds prefix[0..n] = exclusive scan of split counts in LDS; returns total.
@@ -135,6 +162,40 @@ __device__ __forceinline__ int find_row(const int* prefix, int n, int x) {
   return lo;
 }
 
+// Merges the ns >= 2 split partials of (row r, kv head h) into the output.
+// Lane sp holds split sp's (max, sum) (kMaxSplits == 64 == wave size), so the
+// global max and the normaliser are two wave reductions; each dim's
+// accumulator is summed over splits in split order, loads issued eight at a
+// time.  The result depends only on the row's own partials.
+template <typename T>
+__device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int lane) {
+  static_assert(kMaxSplits == 64, "one lane per split");
+  const int G = a.hq / a.hkv;
+  const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
+  for (int j = 0; j < G; ++j) {
+    T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
+    const float2 ml = lane < ns ? a.ws_ml[(slot0 + lane) * G + j] : make_float2(-INFINITY, 0.f);
+    const float M = strided_max<1>(ml.x);
+    const float w = lane < ns ? fast_exp2(ml.x - M) : 0.f;
+    const float inv = 1.f / group_sum<64>(ml.y * w);
+    const float* base = a.ws_acc + (slot0 * G + j) * a.d;
+    const int64_t split_stride = static_cast<int64_t>(G) * a.d;
+    for (int d = lane; d < a.d; d += 64) {
+      float acc = 0.f;
+      int sp = 0;
+      for (; sp + 8 <= ns; sp += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = base[(sp + u) * split_stride + d];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(x[u], __shfl(w, sp + u, 64), acc);
+      }
+      for (; sp < ns; ++sp) acc = fmaf(base[sp * split_stride + d], __shfl(w, sp, 64), acc);
+      store_elem(orow + d * a.o_dim, acc * inv);
+    }
+  }
+}
+
 template <typename T, int D, int G, int P, int TILE>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   using PK = Packet<T>;
@@ -165,6 +226,15 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int len = uniform(row_length(a, r));
     int split_len, ns;
     split_plan(len, &split_len, &ns);
+    if (len <= 0) {
+      if (g == 0) {
+        T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h) * G * a.o_head + lane_dim;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < G; ++j) *reinterpret_cast<u32x4*>(orow + j * a.o_head) = zero;
+      }
+      continue;
+    }
     const int t_begin = sp * split_len;
     const int t_end = min(len, t_begin + split_len);
     const int last = t_end - 1;
@@ -202,30 +272,45 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     // picked out with readlane so every K/V load has a scalar page base.
     int table_chunk = -1;
     int table_entry = 0;
-    for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
+    auto tile_pages = [&](int t0, int64_t (&blk)[PPT]) {
       const int rel0 = (t0 - t_begin) / P;
       if ((rel0 >> 6) != table_chunk) {
         table_chunk = rel0 >> 6;
         const int rel = table_chunk * 64 + lane;
         table_entry = rel <= last_rel_page ? trow[first_page + rel] : 0;
       }
-      u32x4 kp[NI], vp[NI];
 #pragma unroll
       for (int pg = 0; pg < PPT; ++pg) {
         const int rel = min(rel0 + pg, last_rel_page);
-        int64_t blk = __builtin_amdgcn_readlane(table_entry, rel & 63);
-        blk = (blk < 0 || blk >= a.num_blocks) ? 0 : blk;
-        const T* kpage = kbase + blk * a.kv_block;
-        const T* vpage = vbase + blk * a.kv_block;
+        const int64_t b = __builtin_amdgcn_readlane(table_entry, rel & 63);
+        blk[pg] = (b < 0 || b >= a.num_blocks) ? 0 : b;
+      }
+    };
+    auto issue = [&](u32x4 (&dst)[NI], const T* base, const int64_t (&blk)[PPT], int t0) {
+#pragma unroll
+      for (int pg = 0; pg < PPT; ++pg) {
+        const T* page = base + blk[pg] * a.kv_block;
 #pragma unroll
         for (int i = 0; i < IPP; ++i) {
           const int tok = min(t0 + pg * P + i * TPI + g, last);
           const uint32_t off = static_cast<uint32_t>(tok & (P - 1)) * tok_stride + lane_dim;
-          kp[pg * IPP + i] = *reinterpret_cast<const u32x4*>(kpage + off);
-          vp[pg * IPP + i] = *reinterpret_cast<const u32x4*>(vpage + off);
+          dst[pg * IPP + i] = load_page(reinterpret_cast<const u32x4*>(page + off));
         }
       }
+    };
 
+    // Software pipeline: K(t+1) is issued right after the scores of tile t
+    // and V(t+1) right after its value accumulation, so a wave always has
+    // the next tile's loads in flight while it computes, in the same
+    // registers.
+    u32x4 kp[NI], vp[NI];
+    int64_t blk[PPT];
+    tile_pages(t_begin, blk);
+    issue(kp, kbase, blk, t_begin);
+    issue(vp, vbase, blk, t_begin);
+    for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
+      const int t1 = t0 + TILE;
+      const bool more = t1 < t_end;
       float sc[G][NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -240,6 +325,11 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
           dot = group_sum<LPT>(dot);
           sc[j][i] = valid ? dot : -INFINITY;
         }
+      }
+      int64_t next_blk[PPT];
+      if (more) {
+        tile_pages(t1, next_blk);
+        issue(kp, kbase, next_blk, t1);
       }
 
       float p[G][NI];
@@ -271,6 +361,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
           for (int e = 0; e < EPL; ++e) acc[j][e] = fmaf(p[j][i], y[e], acc[j][e]);
       }
+      if (more) issue(vp, vbase, next_blk, t1);
     }
 
     // Merge the token groups (lanes that share s).
@@ -320,43 +411,16 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Merge kernel: one wavefront per (row, kv_head).  Zeroes empty rows and
-// merges multi-split partials in split order; single-split rows are done.
+// Merge kernel: one wavefront per (row, kv_head) with more than one split.
 template <typename T>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (item >= a.n_rows * a.hkv) return;
-  const int lane = threadIdx.x & 63;
   const int r = item / a.hkv;
   const int h = item - r * a.hkv;
   int split_len, ns;
   split_plan(row_length(a, r), &split_len, &ns);
-  if (ns == 1) return;
-  const int G = a.hq / a.hkv;
-  const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
-  for (int j = 0; j < G; ++j) {
-    T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
-    if (ns == 0) {
-      for (int d = lane; d < a.d; d += 64) store_elem(orow + d * a.o_dim, 0.f);
-      continue;
-    }
-    float M = -INFINITY;
-    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, a.ws_ml[(slot0 + sp) * G + j].x);
-    float L = 0.f;
-    for (int sp = 0; sp < ns; ++sp) {
-      const float2 ml = a.ws_ml[(slot0 + sp) * G + j];
-      L += ml.y * fast_exp2(ml.x - M);
-    }
-    const float inv = 1.f / L;
-    for (int d = lane; d < a.d; d += 64) {
-      float acc = 0.f;
-      for (int sp = 0; sp < ns; ++sp) {
-        const float w = fast_exp2(a.ws_ml[(slot0 + sp) * G + j].x - M);
-        acc = fmaf(a.ws_acc[((slot0 + sp) * G + j) * a.d + d], w, acc);
-      }
-      store_elem(orow + d * a.o_dim, acc * inv);
-    }
-  }
+  if (ns > 1) merge_partials<T>(a, r, h, ns, threadIdx.x & 63);
 }
 
 // Generic kernel for shapes the tiled kernel does not cover (odd head_dim,
@@ -428,10 +492,10 @@ using DecodeKernel = void (*)(DecodeArgs);
 template <typename T, int D>
 DecodeKernel pick_group(int G) {
   switch (G) {
-    case 1: return paged_decode_kernel<T, D, 1, 16, 32>;
-    case 2: return paged_decode_kernel<T, D, 2, 16, 32>;
-    case 4: return paged_decode_kernel<T, D, 4, 16, 32>;
-    case 8: return paged_decode_kernel<T, D, 8, 16, 32>;
+    case 1: return paged_decode_kernel<T, D, 1, 16, kTile>;
+    case 2: return paged_decode_kernel<T, D, 2, 16, kTile>;
+    case 4: return paged_decode_kernel<T, D, 4, 16, kTile>;
+    case 8: return paged_decode_kernel<T, D, 8, 16, kTile>;
     default: return nullptr;
   }
 }
@@ -496,13 +560,25 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   return check_launch("rlt_paged_decode(merge)");
 }
 
-int64_t workspace_bytes_for(int64_t rows, int64_t hq, int64_t hkv, int64_t d) {
-  if (rows <= 0 || hq <= 0 || hkv <= 0 || d <= 0 || hq % hkv) return 0;
+int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace layout: acc partials | (max, sum) partials.
+struct WorkspaceLayout {
+  int64_t acc, ml, total;
+};
+WorkspaceLayout workspace_layout(int64_t rows, int64_t hq, int64_t hkv, int64_t d) {
   rows = std::min<int64_t>(rows, kMaxRowsPerLaunch);
   const int64_t slots = rows * hkv * kMaxSplits * (hq / hkv);
-  const int64_t acc = slots * d * static_cast<int64_t>(sizeof(float));
-  const int64_t ml = slots * static_cast<int64_t>(sizeof(float2));
-  return (acc + 255) / 256 * 256 + ml;
+  WorkspaceLayout w{};
+  w.acc = 0;
+  w.ml = round256(slots * d * static_cast<int64_t>(sizeof(float)));
+  w.total = w.ml + round256(slots * static_cast<int64_t>(sizeof(float2)));
+  return w;
+}
+
+int64_t workspace_bytes_for(int64_t rows, int64_t hq, int64_t hkv, int64_t d) {
+  if (rows <= 0 || hq <= 0 || hkv <= 0 || d <= 0 || hq % hkv) return 0;
+  return workspace_layout(rows, hq, hkv, d).total;
 }
 
 }  // namespace
@@ -555,10 +631,10 @@ extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const v
   a.o_row = out_strides[0];
   a.o_head = out_strides[1];
   a.o_dim = out_strides[2];
-  a.ws_acc = static_cast<float*>(workspace);
-  const int64_t rows_cap = std::min<int64_t>(n_rows, kMaxRowsPerLaunch);
-  const int64_t acc_bytes = rows_cap * num_kv_heads * kMaxSplits * (num_q_heads / num_kv_heads) * head_dim * 4;
-  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + (acc_bytes + 255) / 256 * 256);
+  const WorkspaceLayout layout = workspace_layout(n_rows, num_q_heads, num_kv_heads, head_dim);
+  char* ws = static_cast<char*>(workspace);
+  a.ws_acc = reinterpret_cast<float*>(ws + layout.acc);
+  a.ws_ml = reinterpret_cast<float2*>(ws + layout.ml);
   a.hkv = static_cast<int>(num_kv_heads);
   a.hq = static_cast<int>(num_q_heads);
   a.d = static_cast<int>(head_dim);
