@@ -1,0 +1,173 @@
+"""Write golden vectors by running the reference implementation on the CPU.
+
+Run in the build container only (the reference tree is not shipped):
+
+    python tests/golden/make_reference_goldens.py /root/reference
+
+Two fixtures pin what the reference's own tests leave open:
+  allocator_trace.json -- exact physical page ids, refcounts and free counts of
+      KVCacheManager (vllm_rlt/core/kv_cache_manager.py:137-344) after every
+      step of a scripted sequence of allocate / ensure_capacity / free /
+      prefix publish / lookup / eviction / transfer leases, plus the host
+      metadata of _prepare_batch (:398-478) for a few batches.
+  paged_attention_cpu.npz -- inputs and exact output bits of
+      torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36) on
+      seeded bf16 / fp16 / fp32 cases.
+The fixture files hold data only (inputs and outputs).
+"""
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+OUT = Path(__file__).resolve().parent
+
+# Scripted bookkeeping steps.  Each step is [op, *args]; the replay in
+# tests/test_golden_reference.py interprets the same list.
+STEPS = [
+    ["allocate", "r0", 9, None],
+    ["allocate", "r1", 20, 5],
+    ["allocate", "r2", 6, None],
+    ["write_all", "r1", 8],
+    ["ensure", "r1", 13],
+    ["free", "r0"],
+    ["allocate", "r3", 17, 3],
+    ["mark_imported", "r2", 6],
+    ["publish", "r2", [7, 7, 1, 2, 3, 4, 5], 6],
+    ["lookup", [7, 7, 1, 2, 3, 4, 9, 9]],
+    ["allocate_prefix", "r4", 12, None, [7, 7, 1, 2, 3, 4, 9, 9]],
+    ["free", "r2"],
+    ["ensure", "r3", 17],
+    ["pin", "r3", "t0"],
+    ["free", "r3"],
+    ["allocate", "r5", 8, None],
+    ["unpin", "r3", "t0"],
+    ["allocate", "big", 30, None],
+    ["lookup", [7, 7, 1, 2, 3, 4, 9, 9]],
+    ["free", "r4"],
+    ["free", "r1"],
+    ["allocate", "r6", 4, 1],
+    ["free", "big"],
+    ["allocate", "r7", 33, 10],
+]
+
+# Batches planned after the last step: (request ids, depths, positions).
+BATCHES = [
+    (["r6", "r7", "r7", "r5"], [2, 0, 1, 1], [0, 9, 3, 7]),
+    (["r7"] * 3 + ["r5"] * 2, [1, 1, 1, 2, 2], [4, 5, 6, 0, 1]),
+]
+
+
+def snapshot(cache):
+    return {
+        "tables": {rid: [list(t) for t in a.block_tables] for rid, a in sorted(cache._allocations.items())},
+        "free": list(cache._free_blocks),
+        "refs": list(cache._refs),
+        "num_free": cache.num_free_blocks,
+        "prefixes": [list(blocks) for blocks in cache._prefixes.values()],
+    }
+
+
+def allocator_trace():
+    from vllm_rlt.core.kv_cache_manager import KVCacheManager
+
+    cache = KVCacheManager(2, 1, 2, 64, 4, 3, enable_prefix_caching=True)
+    results = []
+    for step in STEPS:
+        op, args = step[0], step[1:]
+        out = None
+        if op == "allocate":
+            rid, max_tokens, initial = args
+            out = cache.allocate(rid, max_tokens, initial_tokens=initial)
+        elif op == "allocate_prefix":
+            rid, max_tokens, initial, tokens = args
+            out = cache.allocate(rid, max_tokens, initial_tokens=initial, prefix=cache.lookup_prefix(tokens))
+        elif op == "ensure":
+            out = cache.ensure_capacity(*args)
+        elif op == "free":
+            cache.free(*args)
+        elif op == "write_all":
+            rid, n = args
+            for plane in cache._allocations[rid].written:
+                for w in plane:
+                    for p in range(n):
+                        w.add(p)
+        elif op == "mark_imported":
+            cache.mark_imported_prefix(*args)
+        elif op == "publish":
+            cache.publish_prefix(*args)
+        elif op == "lookup":
+            out = [list(b) for b in cache.lookup_prefix(args[0])]
+        elif op == "pin":
+            cache.pin_transfer(*args)
+        elif op == "unpin":
+            cache.unpin_transfer(*args)
+        else:
+            raise ValueError(op)
+        results.append({"step": step, "result": out, "state": snapshot(cache)})
+    batches = []
+    for ids, depths, positions in BATCHES:
+        b = cache._prepare_batch(ids, depths, positions)
+        batches.append(
+            {
+                "ids": ids,
+                "depths": depths,
+                "positions": positions,
+                "write_blocks": b.write_blocks.tolist(),
+                "write_offsets": b.write_offsets.tolist(),
+                "block_tables": b.block_tables.tolist(),
+                "context_lengths": b.context_lengths.tolist(),
+            }
+        )
+    config = dict(num_layers=2, num_kv_heads=1, head_dim=2, num_blocks=64, block_size=4, max_loops=3)
+    return {"config": config, "steps": results, "batches": batches}
+
+
+def attention_cases():
+    from vllm_rlt.kernels.paged_attention import torch_paged_attention
+
+    arrays = {}
+    cases = [
+        ("bf16_g1", torch.bfloat16, 4, 4, 32, 16, [0, 1, 37, 100]),
+        ("fp16_g2", torch.float16, 4, 2, 16, 5, [12, 3, 0, 64]),
+        ("fp32_g3", torch.float32, 6, 2, 8, 3, [7, 1, 19, 30]),
+        ("bf16_d128", torch.bfloat16, 2, 2, 128, 16, [300, 17]),
+    ]
+    for name, dtype, hq, hkv, d, page, lengths in cases:
+        g = torch.Generator().manual_seed(len(name) * 7919 + d)
+        pages = [(n + page - 1) // page for n in lengths]
+        nb = sum(pages) + 2
+        perm = torch.randperm(nb, generator=g)
+        tables = torch.full((len(lengths), max(pages + [1])), -1, dtype=torch.int32)
+        used = 0
+        for r, p in enumerate(pages):
+            tables[r, :p] = perm[used : used + p].to(torch.int32)
+            used += p
+        key_cache = (torch.randn(nb, page, hkv, d, generator=g) * 2).to(dtype)
+        value_cache = torch.randn(nb, page, hkv, d, generator=g).to(dtype)
+        q = torch.randn(len(lengths), hq, d, generator=g).to(dtype)
+        lens = torch.tensor(lengths, dtype=torch.int32)
+        out = torch_paged_attention(q, key_cache, value_cache, tables, lens)
+        bits = {torch.bfloat16: torch.int16, torch.float16: torch.int16, torch.float32: torch.int32}[dtype]
+        for field, t in (("q", q), ("k", key_cache), ("v", value_cache), ("out", out)):
+            arrays[f"{name}/{field}"] = t.view(bits).numpy()
+        arrays[f"{name}/tables"] = tables.numpy()
+        arrays[f"{name}/lengths"] = lens.numpy()
+        arrays[f"{name}/dtype"] = np.array(str(dtype).split(".")[-1])
+    return arrays
+
+
+def main():
+    reference = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    sys.path.insert(0, reference)
+    torch.set_num_threads(1)
+    (OUT / "allocator_trace.json").write_text(json.dumps(allocator_trace(), indent=1))
+    np.savez_compressed(OUT / "paged_attention_cpu.npz", **attention_cases())
+    print("wrote", OUT / "allocator_trace.json", OUT / "paged_attention_cpu.npz")
+
+
+if __name__ == "__main__":
+    main()

@@ -6,6 +6,17 @@ include/rlt_kv.h).
 """
 
 from . import ops
+from .device_cache import DeviceCache
+from .kv_cache_manager import KVCacheManager
+from .page_book import KVPageBook, PreparedKVBatch
 from .paged_attention import HipPagedAttention, hip_paged_attention
 
-__all__ = ["HipPagedAttention", "hip_paged_attention", "ops"]
+__all__ = [
+    "DeviceCache",
+    "HipPagedAttention",
+    "KVCacheManager",
+    "KVPageBook",
+    "PreparedKVBatch",
+    "hip_paged_attention",
+    "ops",
+]

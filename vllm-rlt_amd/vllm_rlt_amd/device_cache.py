@@ -1,0 +1,26 @@
+"""Graph-capturable cache proxy for a recurrent core (vllm_rlt/worker/cuda_graph.py:10-29).
+
+DeviceCache exposes only the GPU side of _write_prepared / _attend_prepared:
+no host bookkeeping, no validation that reads device memory, no allocation
+beyond the caching allocator, so a 24-layer core that calls it can be captured
+in a HIP graph and replayed.  The caller owns the written-position records.
+"""
+
+from __future__ import annotations
+
+from . import ops
+
+
+class DeviceCache:
+    def __init__(self, cache):
+        self.cache = cache
+
+    def _write_prepared(self, layer, batch, k, v):
+        cache = self.cache
+        ops.kv_append(cache.key_cache, cache.value_cache, layer, batch.write_blocks, batch.write_offsets, k, v)
+
+    def _attend_prepared(self, layer, batch, q):
+        cache = self.cache
+        return cache.attention(
+            q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths
+        )
