@@ -279,8 +279,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(
-            f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the decode path shards with no "
-            "cross-GPU exchange; see DESIGN.md for the multi-GPU layout)",
+            f"bench.py runs on one GPU: --gpus {args.gpus} is not supported; decode shards by request or "
+            "KV head with no cross-GPU exchange, so one GPU's throughput is the per-GPU figure",
             file=sys.stderr,
         )
         sys.exit(2)

@@ -11,7 +11,7 @@ for path in (REPO, REPO / "vllm-rlt_amd"):
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs a ROCm (gfx950) device; run with -m gpu on the GPU box")
+    config.addinivalue_line("markers", "gpu: needs a ROCm (gfx950) device; select with -m gpu")
 
 
 def pytest_collection_modifyitems(config, items):
