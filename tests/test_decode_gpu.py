@@ -241,3 +241,49 @@ def test_packed_prefill_matches_per_token_oracle(dtype):
         expect = paged_attention_cpu(q, kp[:, layer], vp[:, layer], row_tables, row_lengths)
         atol, rtol = TOL[dtype]
         torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
+
+
+def ragged_prefill_case(dtype, hq, hkv, d, prefixes, chunks, seed):
+    """Packed chunks over paged prefixes with random page permutations, plus its per-token oracle rows."""
+    g = torch.Generator().manual_seed(seed)
+    page = 16
+    lens = [p + c for p, c in zip(prefixes, chunks)]
+    pages = [math.ceil(n / page) for n in lens]
+    nb = sum(pages) + 3
+    perm = torch.randperm(nb, generator=g)
+    key_pool = torch.randn(nb, page, hkv, d, generator=g).to(dtype)
+    value_pool = torch.randn(nb, page, hkv, d, generator=g).to(dtype)
+    width = max(pages)
+    tables = torch.full((len(lens), width), -1, dtype=torch.int32)
+    used = 0
+    for s, p in enumerate(pages):
+        tables[s, :p] = perm[used : used + p].to(torch.int32)
+        used += p
+    q = torch.randn(sum(chunks), hq, d, generator=g).to(dtype)
+    cu = torch.tensor([0] + list(torch.tensor(chunks).cumsum(0).tolist()), dtype=torch.int32)
+    row_tables = torch.cat([tables[s].repeat(c, 1) for s, c in enumerate(chunks)])
+    row_lengths = torch.tensor([p + i + 1 for p, c in zip(prefixes, chunks) for i in range(c)], dtype=torch.int32)
+    return q, key_pool, value_pool, tables, torch.tensor(lens, dtype=torch.int32), cu, row_tables, row_lengths
+
+
+@pytest.mark.parametrize(
+    "dtype,hq,hkv,d",
+    [
+        (torch.bfloat16, 16, 16, 128),
+        (torch.float16, 16, 16, 128),
+        (torch.bfloat16, 8, 4, 128),
+        (torch.bfloat16, 4, 4, 64),
+        (torch.float32, 4, 4, 128),
+    ],
+)
+def test_mfma_prefill_ragged_chunks_over_long_prefixes(dtype, hq, hkv, d):
+    # Chunks that end mid-tile, a one-token chunk, prefixes past several key tiles.
+    from vllm_rlt_amd import ops
+
+    prefixes, chunks = [0, 300, 1000, 2900, 17], [256, 130, 65, 1, 200]
+    q, kp, vp, tables, lens, cu, row_tables, row_lengths = ragged_prefill_case(dtype, hq, hkv, d, prefixes, chunks, 4)
+    out = ops.paged_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), cu.cuda(), max(chunks))
+    torch.cuda.synchronize()
+    expect = paged_attention_cpu(q, kp, vp, row_tables, row_lengths)
+    atol, rtol = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (2e-3, 2e-3), torch.float32: (1e-5, 1e-5)}[dtype]
+    torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)

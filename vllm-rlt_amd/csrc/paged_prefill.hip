@@ -1,11 +1,28 @@
 // Packed chunked-prefill attention over paged prefixes (bottom-right causal).
 //
 // Sequence s owns query rows [cu[s], cu[s+1]); its keys end at its last query
-// position, so query row i sees len_k[s] - (cu[s+1] - 1 - i) keys.  This file
-// expands every query row into a decode row (its own length and a copy of its
-// sequence's table row) in the workspace and runs the split-K decode kernels
-// on them -- the same per-token causal rows the reference's non-FA4 backends
-// use for prefill.
+// position, so chunk query i sees keys [0, len_k[s] - n_q + i].
+//
+// MFMA path (bf16 / fp16, head_dim 64 or 128, page 16).  A workgroup owns 128
+// query rows of one (sequence, query head); each of its 4 waves owns 32.  Key
+// tiles of 64 tokens (4 pages) are staged in LDS -- K row-major, V transposed
+// -- with the next tile's global loads in registers while the current tile
+// computes.  Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = K
+// rows from LDS, B = its 32 q rows from registers), so every lane holds 16
+// keys of one query: the online softmax needs one exchange with the lane 32
+// away.  The exponentiated scores, rounded to the storage type, are already
+// the B operand of O^T += V^T P^T: within each 16-key k-step lane half h
+// element e holds key 16ks + 8(e/4) + 4h + e%4, and V^T's A operand is read
+// from LDS in that same key order (two 8-byte reads).  Only diagonal tiles are
+// masked; tiles past a wave's last visible key are skipped.  Keys past the
+// sequence re-read its last valid token, so no unwritten page is read.
+// Workgroups are mapped XCD-major so one (head, sequence)'s query tiles share
+// an L2 while they stream the same prefix.
+//
+// Other shapes expand each query row into a decode row (its own key length and
+// a copy of its sequence's table row) in the workspace and run the split-K
+// decode kernels -- the per-token causal rows the reference's non-FA4
+// backends use for prefill.
 #include <algorithm>
 
 #include "common.hpp"
@@ -42,6 +59,251 @@ __global__ __launch_bounds__(kThreads) void expand_rows_kernel(ExpandArgs a) {
   const int32_t* src = a.tables + s * a.table_stride;
   int32_t* dst = a.row_tables + static_cast<int64_t>(row) * a.width;
   for (int64_t c = threadIdx.x; c < a.width; c += kThreads) dst[c] = src[c];
+}
+
+// ---------------------------------------------------------------------------
+// MFMA prefill kernel.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 128;  // query rows per workgroup
+constexpr int kBN = 64;   // keys per tile
+constexpr int kPage = 16;
+constexpr int kXcds = 8;
+constexpr float kLog2eP = 1.4426950408889634f;
+
+bool stride16(int64_t stride, int esize) { return (stride * esize) % 16 == 0; }
+
+struct PrefillArgs {
+  const void* q;
+  int64_t q_row, q_head;
+  const void* k;
+  const void* v;
+  int64_t kv_block, kv_token, kv_head;
+  const int32_t* tables;
+  int64_t table_stride, width;
+  const int32_t* lens;
+  const int32_t* cu;
+  void* out;
+  int64_t o_row, o_head;
+  int num_seqs, hq, hkv;
+  int64_t num_blocks;
+  int total_items;  // grid work items actually launched
+  float qscale;     // scale * log2(e)
+};
+
+template <typename T> struct MfmaOps;
+template <> struct MfmaOps<bf16> {
+  using V8 = bf16x8;
+  __device__ static f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+  __device__ static uint32_t pack2(float x, float y) { return f32_to_bf16_bits(x) | (f32_to_bf16_bits(y) << 16); }
+  __device__ static void store4(void* p, const float* x) {
+    u32x2 w = {pack2(x[0], x[1]), pack2(x[2], x[3])};
+    *reinterpret_cast<u32x2*>(p) = w;
+  }
+};
+template <> struct MfmaOps<f16> {
+  using V8 = f16x8;
+  __device__ static f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+  __device__ static uint32_t pack2(float x, float y) { return f16_bits(x) | (f16_bits(y) << 16); }
+  __device__ static void store4(void* p, const float* x) {
+    u32x2 w = {pack2(x[0], x[1]), pack2(x[2], x[3])};
+    *reinterpret_cast<u32x2*>(p) = w;
+  }
+};
+
+template <typename V8>
+__device__ __forceinline__ V8 as_v8(u32x4 x) {
+  return __builtin_bit_cast(V8, x);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) {
+  using Ops = MfmaOps<T>;
+  using V8 = typename Ops::V8;
+  constexpr int KSTEPS = D / 16;  // q.k k-steps
+  constexpr int DTILES = D / 32;  // output column tiles
+  constexpr int KROW = D + 8;     // LDS K row stride (elements): 16-byte pad
+  constexpr int VROW = kBN + 4;   // LDS V^T row stride (elements): 8-byte pad
+  constexpr int CHUNKS = D / 8;   // 16-byte chunks per token row
+  constexpr int TOKENS_PER_PASS = 256 / CHUNKS;
+  constexpr int PASSES = kBN / TOKENS_PER_PASS;
+  static_assert(kBN % TOKENS_PER_PASS == 0, "tile loads");
+  __shared__ __align__(16) uint16_t k_lds[kBN * KROW];
+  __shared__ __align__(16) uint16_t vt_lds[D * VROW];
+
+  // XCD-major work mapping: xcd x gets a contiguous run of the work list
+  // (gridDim.x is a multiple of kXcds, so this is a bijection).
+  const int per_xcd = gridDim.x / kXcds;
+  const int w = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (w >= a.total_items) return;
+  // Work list: head-major, then query tiles of sequences in order.
+  int tiles_total = 0;
+  for (int s = 0; s < a.num_seqs; ++s) tiles_total += (a.cu[s + 1] - a.cu[s] + kBM - 1) / kBM;
+  if (tiles_total == 0) return;
+  const int h = w / tiles_total;
+  int t = w - h * tiles_total;
+  if (h >= a.hq) return;
+  int seq = 0;
+  for (; seq < a.num_seqs; ++seq) {
+    const int n = (a.cu[seq + 1] - a.cu[seq] + kBM - 1) / kBM;
+    if (t < n) break;
+    t -= n;
+  }
+  if (seq == a.num_seqs) return;
+  const int row0 = a.cu[seq];
+  const int nq = a.cu[seq + 1] - row0;
+  const int64_t max_len = a.width * kPage;
+  const int len_k = static_cast<int>(min<int64_t>(a.lens[seq], max_len));
+  const int prefix = len_k - nq;
+  const int kvh = h / (a.hq / a.hkv);
+  const int qt0 = t * kBM;                         // first chunk row of the workgroup
+  const int wg_last_row = min(qt0 + kBM, nq) - 1;  // last chunk row of the workgroup
+  const int wg_keys = prefix + wg_last_row + 1;
+  if (wg_keys <= 0) return;
+  const int ntiles = (wg_keys + kBN - 1) / kBN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const int wave_row0 = qt0 + wave * 32;  // chunk row of the wave's column 0
+  const bool wave_live = wave_row0 < nq;
+  const int wave_last_key = prefix + min(wave_row0 + 31, nq - 1);
+  const int my_row = wave_row0 + col;
+  const bool row_valid = my_row < nq;
+  const int my_key_limit = prefix + my_row;  // last visible key of this lane's query
+
+  // Q^T B-operands: lane holds dims [ks*16 + half*8, +8) of query my_row.
+  u32x4 qb[KSTEPS];
+  {
+    const int r = row0 + min(my_row, nq - 1);
+    const T* qrow = static_cast<const T*>(a.q) + r * a.q_row + static_cast<int64_t>(h) * a.q_head;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
+  }
+
+  const int32_t* trow = a.tables + static_cast<int64_t>(seq) * a.table_stride;
+  const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(kvh) * a.kv_head;
+  const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(kvh) * a.kv_head;
+  const int ld_tok = tid / CHUNKS;
+  const int ld_chunk = tid % CHUNKS;
+  u32x4 kreg[PASSES], vreg[PASSES];
+  auto load_tile = [&](int j) {
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+      const int tok = min(j * kBN + i * TOKENS_PER_PASS + ld_tok, len_k - 1);
+      int64_t blk = trow[tok / kPage];
+      blk = (blk < 0 || blk >= a.num_blocks) ? 0 : blk;
+      const int64_t off = blk * a.kv_block + static_cast<int64_t>(tok % kPage) * a.kv_token + ld_chunk * 8;
+      kreg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + off));
+      vreg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + off));
+    }
+  };
+
+  f32x16 acc_o[DTILES];
+#pragma unroll
+  for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;
+
+  load_tile(0);
+  for (int j = 0; j < ntiles; ++j) {
+    __syncthreads();  // everyone is done reading the previous tile
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+      const int tok = i * TOKENS_PER_PASS + ld_tok;
+      *reinterpret_cast<u32x4*>(&k_lds[tok * KROW + ld_chunk * 8]) = kreg[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt_lds[(ld_chunk * 8 + 2 * e) * VROW + tok] = static_cast<uint16_t>(vreg[i][e] & 0xffffu);
+        vt_lds[(ld_chunk * 8 + 2 * e + 1) * VROW + tok] = static_cast<uint16_t>(vreg[i][e] >> 16);
+      }
+    }
+    __syncthreads();
+    if (j + 1 < ntiles) load_tile(j + 1);
+    const int key0 = j * kBN;
+    if (!wave_live || key0 > wave_last_key) continue;
+
+    // S^T = K Q^T for the tile's two 32-key halves.
+    f32x16 sacc[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      f32x16 c = {};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
+        c = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c);
+      }
+      sacc[hh] = c;
+    }
+    // Scale, mask (diagonal tiles only), online softmax for query my_row.
+    const bool needs_mask = key0 + kBN - 1 > prefix + wave_row0 || !row_valid;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = sacc[hh][r] * a.qscale;
+        if (needs_mask) {
+          const int key = key0 + hh * 32 + (r / 4) * 8 + half * 4 + (r % 4);
+          if (key > my_key_limit || !row_valid) x = -INFINITY;
+        }
+        sacc[hh][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, xor_lane(tmax, 32));
+    const float mn = fmaxf(m, tmax);
+    const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+    float psum = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = (sacc[hh][r] == -INFINITY) ? 0.f : fast_exp2(sacc[hh][r] - mn);
+        sacc[hh][r] = p;
+        psum += p;
+      }
+    lsum = lsum * corr + psum;
+    m = mn;
+#pragma unroll
+    for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
+
+    // O^T += V^T P^T over the tile's four 16-key k-steps.
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int hh = ks / 2, base = (ks % 2) * 8;
+      u32x4 pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pb[e] = Ops::pack2(sacc[hh][base + 2 * e], sacc[hh][base + 2 * e + 1]);
+#pragma unroll
+      for (int c = 0; c < DTILES; ++c) {
+        const uint16_t* vrow = &vt_lds[(c * 32 + col) * VROW + ks * 16 + half * 4];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+        const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
+        acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
+      }
+    }
+  }
+
+  const float total = lsum + xor_lane(lsum, 32);
+  if (!wave_live || !row_valid) return;
+  const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key is written as zeros
+  T* orow = static_cast<T*>(a.out) + (row0 + my_row) * a.o_row + static_cast<int64_t>(h) * a.o_head;
+#pragma unroll
+  for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = acc_o[c][g * 4 + e] * inv;
+      Ops::store4(orow + c * 32 + g * 8 + half * 4, x);
+    }
 }
 
 int64_t expand_bytes(int64_t total_q, int64_t width) {
@@ -85,6 +347,62 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     return fail(RLT_EWORKSPACE, "rlt_paged_prefill: workspace of %lld bytes < required %lld",
                 (long long)workspace_bytes, (long long)need);
   if (!aligned16(workspace)) return fail(RLT_EINVAL, "rlt_paged_prefill: workspace must be 16-byte aligned");
+  if (!q || !key_cache || !value_cache || !out || !q_strides || !kv_strides || !out_strides)
+    return fail(RLT_EINVAL, "rlt_paged_prefill: NULL pointer argument");
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(RLT_EINVAL, "rlt_paged_prefill: query heads must be a positive multiple of KV heads");
+  if (head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
+    return fail(RLT_EINVAL, "rlt_paged_prefill: head_dim, page_size and num_blocks must be positive");
+
+  const int esize = dtype_size(dtype);
+  const bool mfma_ok = (dtype == RLT_BFLOAT16 || dtype == RLT_FLOAT16) && (head_dim == 64 || head_dim == 128) &&
+                       page_size == kPage && q_strides[2] == 1 && out_strides[2] == 1 && kv_strides[3] == 1 &&
+                       aligned16(q) && aligned16(out) && aligned16(key_cache) && aligned16(value_cache) &&
+                       stride16(q_strides[0], esize) && stride16(q_strides[1], esize) &&
+                       stride16(out_strides[0], esize) && stride16(out_strides[1], esize) &&
+                       stride16(kv_strides[0], esize) && stride16(kv_strides[1], esize) &&
+                       stride16(kv_strides[2], esize) && max_table_width > 0 && num_q_heads <= 4096;
+  if (mfma_ok) {
+    PrefillArgs p{};
+    p.q = q;
+    p.q_row = q_strides[0];
+    p.q_head = q_strides[1];
+    p.k = key_cache;
+    p.v = value_cache;
+    p.kv_block = kv_strides[0];
+    p.kv_token = kv_strides[1];
+    p.kv_head = kv_strides[2];
+    p.tables = block_tables;
+    p.table_stride = table_stride;
+    p.width = max_table_width;
+    p.lens = context_lengths;
+    p.cu = cu_seqlens_q;
+    p.out = out;
+    p.o_row = out_strides[0];
+    p.o_head = out_strides[1];
+    p.num_seqs = static_cast<int>(num_seqs);
+    p.hq = static_cast<int>(num_q_heads);
+    p.hkv = static_cast<int>(num_kv_heads);
+    p.num_blocks = num_blocks;
+    p.qscale = scale * kLog2eP;
+    const int64_t tiles_bound = (total_q + kBM - 1) / kBM + num_seqs;
+    const int64_t items = tiles_bound * num_q_heads;
+    if (items > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_paged_prefill: too many query tiles");
+    p.total_items = static_cast<int>(items);
+    // The XCD-major remap is a bijection only on a multiple of 8 workgroups;
+    // the extra ones exit on the item bound.
+    const dim3 grid(static_cast<unsigned>((items + kXcds - 1) / kXcds * kXcds));
+    hipStream_t st = as_stream(stream);
+    if (dtype == RLT_BFLOAT16) {
+      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
+    } else {
+      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 128>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 64>), grid, dim3(256), 0, st, p);
+    }
+    return check_launch("rlt_paged_prefill");
+  }
+
   const int64_t width = std::max<int64_t>(max_table_width, 1);
   char* ws = static_cast<char*>(workspace);
   ExpandArgs e{};
