@@ -39,10 +39,14 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 LAYERS, HQ, HKV, HEAD_DIM, PAGE, LOOPS = 24, 16, 16, 128, 16, 4
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 WORKLOADS = {
     "ouro-last-exited": dict(batch=64, ctx=(512, 4096), planes=LOOPS, depth_probs=None),
     "ouro-shared": dict(batch=256, ctx=(1024, 8192), planes=1, depth_probs=(0.1, 0.2, 0.3, 0.4)),
 }
+# Chunked prefill: 8 sequences x 512 new tokens over prefixes U[0, 16384], the
+# full 4-loop prefill (4 depths x 24 layers of append + packed attention).
+PREFILL = dict(seqs=8, chunk=512, prefix=(0, 16384))
 
 
 def parse_args():
@@ -50,7 +54,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", choices=sorted(WORKLOADS), default="ouro-last-exited")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["ouro-prefill"], default="ouro-last-exited")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-reps", type=int, default=3, help="timed repetitions of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -275,6 +279,171 @@ def cpu_baseline(w, step, reps):
     }
 
 
+class PrefillWorkload:
+    """LAST-EXITED pool, per-depth packed-prefill metadata and per-layer chunk projections."""
+
+    def __init__(self, seed, device):
+        g = torch.Generator().manual_seed(seed)
+        n, chunk = PREFILL["seqs"], PREFILL["chunk"]
+        lo, hi = PREFILL["prefix"]
+        self.prefixes = torch.randint(lo, hi + 1, (n,), generator=g)
+        self.lens = self.prefixes + chunk
+        pages = (self.lens + PAGE - 1) // PAGE
+        self.width = int(pages.max())
+        self.num_blocks = int(pages.sum()) * LOOPS
+        perm = torch.randperm(self.num_blocks, generator=g)
+        tables = torch.zeros(n, LOOPS, self.width, dtype=torch.int32)
+        used = 0
+        for s in range(n):
+            for plane in range(LOOPS):
+                k = int(pages[s])
+                tables[s, plane, :k] = perm[used : used + k].to(torch.int32)
+                used += k
+        rows = torch.arange(n).repeat_interleave(chunk)
+        pos = (self.prefixes[rows] + torch.arange(chunk).repeat(n)).long()
+        self.depth_blocks = [tables[rows, d, pos // PAGE].long().to(device) for d in range(LOOPS)]
+        self.offsets = (pos % PAGE).to(device)
+        self.depth_tables = [tables[:, d].contiguous().to(device) for d in range(LOOPS)]
+        self.context_lengths = self.lens.to(torch.int32).to(device)
+        self.cu = torch.arange(0, (n + 1) * chunk, chunk, dtype=torch.int32).to(device)
+        shape = (self.num_blocks, LAYERS, PAGE, HKV, HEAD_DIM)
+        self.key_cache = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        self.value_cache = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        gen = torch.Generator(device=device).manual_seed(seed + 1)
+        for pool in (self.key_cache, self.value_cache):
+            flat = pool.view(-1)
+            for start in range(0, flat.numel(), 1 << 28):
+                flat[start : start + (1 << 28)].normal_(generator=gen)
+        total = n * chunk
+        self.q = torch.randn((LAYERS, total, HQ, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        self.k_new = torch.randn((LAYERS, total, HKV, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        self.v_new = torch.randn((LAYERS, total, HKV, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        self.out = torch.empty_like(self.q)
+
+    def flops(self):
+        """Visible (query, key) pairs x 4 * Hq * D over 4 depths x 24 layers (QK^T and PV)."""
+        chunk = PREFILL["chunk"]
+        pairs = sum(chunk * int(p) + chunk * (chunk + 1) // 2 for p in self.prefixes)
+        return 4 * HQ * HEAD_DIM * pairs * LOOPS * LAYERS
+
+    def layer(self, depth, layer, events=None):
+        from vllm_rlt_amd import ops
+
+        ops.kv_append(
+            self.key_cache, self.value_cache, layer, self.depth_blocks[depth], self.offsets,
+            self.k_new[layer], self.v_new[layer],
+        )
+        if events is not None:
+            events[0].record()
+        ops.paged_prefill(
+            self.q[layer], self.key_cache[:, layer], self.value_cache[:, layer], self.depth_tables[depth],
+            self.context_lengths, self.cu, PREFILL["chunk"], out=self.out[layer],
+        )
+        if events is not None:
+            events[1].record()
+
+    def step(self):
+        for depth in range(LOOPS):
+            for layer in range(LAYERS):
+                self.layer(depth, layer)
+
+
+def prefill_spot_check(w):
+    """Parity of the last (depth 3, layer 23) prefill on a few query rows against the CPU oracle."""
+    from oracle.paged_attention import paged_attention_cpu
+
+    torch.cuda.synchronize()
+    chunk = PREFILL["chunk"]
+    picks = [(0, 0), (0, chunk - 1), (PREFILL["seqs"] - 1, chunk // 2)]
+    tables = w.depth_tables[LOOPS - 1].cpu()
+    worst = 0.0
+    for s, i in picks:
+        n = int(w.prefixes[s]) + i + 1
+        pages = [int(b) for b in tables[s, : (n + PAGE - 1) // PAGE]]
+        idx = torch.tensor(pages, device=w.key_cache.device)
+        kc = w.key_cache[idx, LAYERS - 1].cpu()
+        vc = w.value_cache[idx, LAYERS - 1].cpu()
+        local = torch.arange(len(pages), dtype=torch.int32)[None]
+        row = s * chunk + i
+        expect = paged_attention_cpu(w.q[LAYERS - 1][row : row + 1].cpu(), kc, vc, local, torch.tensor([n], dtype=torch.int32))
+        got = w.out[LAYERS - 1][row : row + 1].cpu()
+        err = (got.float() - expect.float()).abs().max().item()
+        if not torch.allclose(got.float(), expect.float(), atol=2e-2, rtol=1e-2):
+            raise SystemExit(f"prefill parity spot check failed at seq {s} row {i}: max-abs {err}")
+        worst = max(worst, err)
+    return worst
+
+
+def run_prefill(args, device):
+    t_setup = time.perf_counter()
+    w = PrefillWorkload(args.seed, device)
+    torch.cuda.synchronize()
+    print(
+        f"[bench] workload ouro-prefill: {PREFILL['seqs']} x {PREFILL['chunk']} tokens, prefixes "
+        f"{w.prefixes.tolist()}, pool {2 * w.key_cache.numel() * 2 / 1e9:.1f} GB, setup "
+        f"{time.perf_counter() - t_setup:.1f}s",
+        file=sys.stderr,
+        flush=True,
+    )
+    for step in range(args.warmup):
+        w.step()
+        if step == 0 and not args.no_check:
+            err = prefill_spot_check(w)
+            print(f"[bench] prefill parity spot check ok (max-abs {err:.3g})", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        w.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    pairs = []
+    for _ in range(args.steps):
+        for depth in range(LOOPS):
+            for layer in range(LAYERS):
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                w.layer(depth, layer, ev)
+                pairs.append(ev)
+    torch.cuda.synchronize()
+    launch_ms = statistics.fmean(a.elapsed_time(b) for a, b in pairs)
+    flops = w.flops()
+    launch_tflops = flops / (LOOPS * LAYERS) / (launch_ms * 1e-3) / 1e12
+    step_tflops = flops * args.steps / elapsed / 1e12
+    line = {
+        "metric": "chunked prefill attention: bf16 MFMA TFLOP/s (% of dense peak)",
+        "value": round(step_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"ouro-prefill: {PREFILL['seqs']} sequences x {PREFILL['chunk']} new tokens over prefixes "
+            f"U{list(PREFILL['prefix'])}, 16/16 heads, head_dim 128, page 16, LAST-EXITED, step = 4 depths x 24 "
+            "layers x (chunk KV append + packed causal prefill attention)",
+            "global_batch": PREFILL["seqs"],
+            "seq_len": PREFILL["chunk"],
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "kernel": "rlt_paged_prefill (paged_prefill_mfma_kernel)",
+            "bound": "mfma",
+            "achieved": round(launch_tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(launch_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(launch_ms, 5),
+            "algorithmic_flops_per_launch": int(flops / (LOOPS * LAYERS)),
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -297,6 +466,9 @@ def main():
     device = torch.device("cuda:0")
     if args.calibrate_counters:
         calibrate_counters(device)
+        return
+    if args.workload == "ouro-prefill":
+        run_prefill(args, device)
         return
     total = args.warmup + args.steps
     t_setup = time.perf_counter()

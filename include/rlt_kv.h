@@ -108,10 +108,15 @@ int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_ca
                      int64_t num_blocks, float scale, int dtype, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes rlt_paged_prefill needs (shape-only, no sync needed). */
+/*
+ * Workspace bytes rlt_paged_prefill needs (shape-only, no sync needed).  Zero
+ * for the MFMA path (bf16/fp16, head_dim 64 or 128, page 16, 16-byte aligned
+ * rows); otherwise the size of the per-token decode-row path.
+ */
 int64_t rlt_paged_prefill_workspace_bytes(int64_t total_q, int64_t num_seqs,
                                           int64_t max_table_width, int64_t num_q_heads,
-                                          int64_t num_kv_heads, int64_t head_dim);
+                                          int64_t num_kv_heads, int64_t head_dim,
+                                          int64_t page_size, int dtype);
 
 /*
  * Packed chunked-prefill attention over paged prefixes, bottom-right causal.

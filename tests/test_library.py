@@ -73,7 +73,9 @@ def test_workspace_sizes_depend_only_on_shape():
     assert lib.rlt_paged_decode_workspace_bytes(64, 16, 16, 128) == one
     assert lib.rlt_paged_decode_workspace_bytes(128, 16, 16, 128) > one
     assert lib.rlt_paged_decode_workspace_bytes(0, 16, 16, 128) == 0
-    assert lib.rlt_paged_prefill_workspace_bytes(4096, 8, 1057, 16, 16, 128) > 0
+    # bf16, head_dim 128, page 16: the MFMA path needs no workspace; fp32 takes the decode-row path.
+    assert lib.rlt_paged_prefill_workspace_bytes(4096, 8, 1057, 16, 16, 128, 16, 2) == 0
+    assert lib.rlt_paged_prefill_workspace_bytes(4096, 8, 1057, 16, 16, 128, 16, 0) > 0
 
 
 def test_ops_refuse_cpu_tensors():

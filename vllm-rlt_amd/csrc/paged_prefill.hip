@@ -317,11 +317,25 @@ int64_t expand_bytes(int64_t total_q, int64_t width) {
 
 using namespace rlt;
 
+namespace rlt {
+namespace {
+// Shapes the MFMA kernel takes (it then needs no workspace), given 16-byte
+// aligned q / out / cache rows.
+bool mfma_shape(int64_t head_dim, int64_t page_size, int dtype) {
+  return (dtype == RLT_BFLOAT16 || dtype == RLT_FLOAT16) && (head_dim == 64 || head_dim == 128) && page_size == kPage;
+}
+int64_t fallback_workspace(int64_t total_q, int64_t width, int64_t hq, int64_t hkv, int64_t d) {
+  return expand_bytes(total_q, width) + rlt_paged_decode_workspace_bytes(total_q, hq, hkv, d);
+}
+}  // namespace
+}  // namespace rlt
+
 extern "C" int64_t rlt_paged_prefill_workspace_bytes(int64_t total_q, int64_t num_seqs, int64_t max_table_width,
-                                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
+                                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                                     int64_t page_size, int dtype) {
   if (total_q <= 0 || num_seqs <= 0) return 0;
-  return expand_bytes(total_q, max_table_width) +
-         rlt_paged_decode_workspace_bytes(total_q, num_q_heads, num_kv_heads, head_dim);
+  if (mfma_shape(head_dim, page_size, dtype)) return 0;
+  return fallback_workspace(total_q, max_table_width, num_q_heads, num_kv_heads, head_dim);
 }
 
 extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const void* key_cache,
@@ -341,12 +355,6 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     return fail(RLT_EINVAL, "rlt_paged_prefill: NULL pointer argument");
   if (total_q > 0x7fffffff || num_seqs > 0x7fffffff)
     return fail(RLT_EUNSUPPORTED, "rlt_paged_prefill: too many rows");
-  const int64_t need = rlt_paged_prefill_workspace_bytes(total_q, num_seqs, max_table_width, num_q_heads,
-                                                         num_kv_heads, head_dim);
-  if (!workspace || workspace_bytes < need)
-    return fail(RLT_EWORKSPACE, "rlt_paged_prefill: workspace of %lld bytes < required %lld",
-                (long long)workspace_bytes, (long long)need);
-  if (!aligned16(workspace)) return fail(RLT_EINVAL, "rlt_paged_prefill: workspace must be 16-byte aligned");
   if (!q || !key_cache || !value_cache || !out || !q_strides || !kv_strides || !out_strides)
     return fail(RLT_EINVAL, "rlt_paged_prefill: NULL pointer argument");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
@@ -355,8 +363,7 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     return fail(RLT_EINVAL, "rlt_paged_prefill: head_dim, page_size and num_blocks must be positive");
 
   const int esize = dtype_size(dtype);
-  const bool mfma_ok = (dtype == RLT_BFLOAT16 || dtype == RLT_FLOAT16) && (head_dim == 64 || head_dim == 128) &&
-                       page_size == kPage && q_strides[2] == 1 && out_strides[2] == 1 && kv_strides[3] == 1 &&
+  const bool mfma_ok = mfma_shape(head_dim, page_size, dtype) && q_strides[2] == 1 && out_strides[2] == 1 && kv_strides[3] == 1 &&
                        aligned16(q) && aligned16(out) && aligned16(key_cache) && aligned16(value_cache) &&
                        stride16(q_strides[0], esize) && stride16(q_strides[1], esize) &&
                        stride16(out_strides[0], esize) && stride16(out_strides[1], esize) &&
@@ -403,6 +410,13 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     return check_launch("rlt_paged_prefill");
   }
 
+  const int64_t need = fallback_workspace(total_q, max_table_width, num_q_heads, num_kv_heads, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(RLT_EWORKSPACE,
+                "rlt_paged_prefill: workspace of %lld bytes < required %lld (the MFMA path, which needs none, "
+                "requires 16-byte aligned q/out/cache rows and head_dim 64/128, page 16, bf16/fp16)",
+                (long long)workspace_bytes, (long long)need);
+  if (!aligned16(workspace)) return fail(RLT_EINVAL, "rlt_paged_prefill: workspace must be 16-byte aligned");
   const int64_t width = std::max<int64_t>(max_table_width, 1);
   char* ws = static_cast<char*>(workspace);
   ExpandArgs e{};

@@ -164,6 +164,12 @@ def paged_decode(
     return out
 
 
+def _rows_aligned16(t: torch.Tensor) -> bool:
+    """Innermost dim contiguous and every row start 16-byte aligned."""
+    size = t.element_size()
+    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((st * size) % 16 == 0 for st in t.stride()[:-1])
+
+
 def paged_prefill(
     q: torch.Tensor,
     key_cache: torch.Tensor,
@@ -202,8 +208,11 @@ def paged_prefill(
         return out
     width = block_tables.shape[1]
     lib = _native.load()
-    need = int(lib.rlt_paged_prefill_workspace_bytes(total, nseq, width, hq, hkv, d))
-    workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    code = dtype_code(q.dtype)
+    if not all(_rows_aligned16(t) for t in (q, out, key_cache, value_cache)):
+        code = _native.RLT_FLOAT32  # the MFMA path needs 16-byte rows; size the per-token fallback
+    need = int(lib.rlt_paged_prefill_workspace_bytes(total, nseq, width, hq, hkv, d, page, code))
+    workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     rc = lib.rlt_paged_prefill(
         q.data_ptr(),
