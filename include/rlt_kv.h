@@ -127,7 +127,8 @@ int64_t rlt_paged_prefill_workspace_bytes(int64_t total_q, int64_t num_seqs,
  * [cu_seqlens_q[s], cu_seqlens_q[s+1]) of q and attends through
  * block_tables[s]; context_lengths[s] is its key length (prefix + chunk), so
  * query row i sees the first context_lengths[s] - (cu[s+1] - 1 - i) keys.
- * The chunk's own K/V must already be in the pool.
+ * The chunk's own K/V must already be in the pool.  scale must be finite and
+ * nonzero (RLT_EINVAL otherwise); negative scales are exact.
  *   cu_seqlens_q: device int32 [num_seqs + 1], cu[0] == 0, cu[num_seqs] == total_q.
  *   block_tables: device int32 [num_seqs, max_table_width] (row stride table_stride).
  */

@@ -259,6 +259,11 @@ def ragged_prefill_case(dtype, hq, hkv, d, prefixes, chunks, seed):
     for s, p in enumerate(pages):
         tables[s, :p] = perm[used : used + p].to(torch.int32)
         used += p
+    # Slots past each sequence's last key hold NaN: the kernels must not read them.
+    for s, n in enumerate(lens):
+        if n % page:
+            key_pool[int(tables[s, pages[s] - 1]), n % page :] = float("nan")
+            value_pool[int(tables[s, pages[s] - 1]), n % page :] = float("nan")
     q = torch.randn(sum(chunks), hq, d, generator=g).to(dtype)
     cu = torch.tensor([0] + list(torch.tensor(chunks).cumsum(0).tolist()), dtype=torch.int32)
     row_tables = torch.cat([tables[s].repeat(c, 1) for s, c in enumerate(chunks)])
@@ -287,3 +292,22 @@ def test_mfma_prefill_ragged_chunks_over_long_prefixes(dtype, hq, hkv, d):
     expect = paged_attention_cpu(q, kp, vp, row_tables, row_lengths)
     atol, rtol = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (2e-3, 2e-3), torch.float32: (1e-5, 1e-5)}[dtype]
     torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_mfma_prefill_negative_scale_negates_scores(d):
+    # scale -1/sqrt(d) over q equals the reference's 1/sqrt(d) over -q (sign flips are exact).
+    from vllm_rlt_amd import ops
+
+    prefixes, chunks = [70, 0, 513], [129, 64, 33]
+    q, kp, vp, tables, lens, cu, row_tables, row_lengths = ragged_prefill_case(
+        torch.bfloat16, 8, 8, d, prefixes, chunks, 9
+    )
+    out = ops.paged_prefill(
+        q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), cu.cuda(), max(chunks), scale=-(d**-0.5)
+    )
+    torch.cuda.synchronize()
+    expect = paged_attention_cpu(-q, kp, vp, row_tables, row_lengths)
+    torch.testing.assert_close(out.cpu(), expect, atol=2e-2, rtol=1e-2)
+    with pytest.raises(ValueError, match="scale"):
+        ops.paged_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), cu.cuda(), 129, scale=0.0)

@@ -5,16 +5,19 @@
 //
 // MFMA path (bf16 / fp16, head_dim 64 or 128, page 16).  A workgroup owns 128
 // query rows of one (sequence, query head); each of its 4 waves owns 32.  Key
-// tiles of 64 tokens (4 pages) are staged in LDS -- K row-major, V transposed
-// -- with the next tile's global loads in registers while the current tile
-// computes.  Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = K
-// rows from LDS, B = its 32 q rows from registers), so every lane holds 16
-// keys of one query: the online softmax needs one exchange with the lane 32
-// away.  The exponentiated scores, rounded to the storage type, are already
-// the B operand of O^T += V^T P^T: within each 16-key k-step lane half h
-// element e holds key 16ks + 8(e/4) + 4h + e%4, and V^T's A operand is read
-// from LDS in that same key order (two 8-byte reads).  Only diagonal tiles are
-// masked; tiles past a wave's last visible key are skipped.  Keys past the
+// tiles of 64 tokens (4 pages) are staged in LDS -- K and V row-major, rows
+// padded against bank conflicts -- with the next tile's global loads in
+// registers while the current tile computes.  Per tile a wave forms
+// S^T = K Q^T with v_mfma_f32_32x32x16 (A = K rows from LDS, B = its 32 q rows
+// from registers), so every lane holds 16 keys of one query: the online
+// softmax needs one exchange with the lane 32 away.  The exponentiated scores,
+// rounded to the storage type, are already the B operand of O^T += V^T P^T:
+// within each 16-key k-step lane half h element e holds key
+// 16ks + 8(e/4) + 4h + e%4, and V^T's A operand is read from row-major V in
+// that same key order with transposing LDS reads (ds_read_b64_tr_b16).  The
+// running maximum moves only when a tile's maximum exceeds it by more than
+// 2^kRescale, so the rescale of the accumulators is rare.  Only diagonal tiles
+// are masked; tiles past a wave's last visible key are skipped.  Keys past the
 // sequence re-read its last valid token, so no unwritten page is read.
 // Workgroups are mapped XCD-major so one (head, sequence)'s query tiles share
 // an L2 while they stream the same prefix.
@@ -24,6 +27,7 @@
 // decode kernels -- the per-token causal rows the reference's non-FA4
 // backends use for prefill.
 #include <algorithm>
+#include <cmath>
 
 #include "common.hpp"
 
@@ -64,15 +68,24 @@ __global__ __launch_bounds__(kThreads) void expand_rows_kernel(ExpandArgs a) {
 // ---------------------------------------------------------------------------
 // MFMA prefill kernel.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kPage = 16;
 constexpr int kXcds = 8;
 constexpr float kLog2eP = 1.4426950408889634f;
+// A row's running maximum is only moved (and its sums rescaled) when a tile's
+// maximum exceeds it by more than this many powers of two; until then the
+// exponentials stay below 2^kRescale, exact enough in fp32 sums and in the
+// bf16/fp16 P operand.
+constexpr float kRescale = 8.f;
 
 bool stride16(int64_t stride, int esize) { return (stride * esize) % 16 == 0; }
 
@@ -81,7 +94,7 @@ struct PrefillArgs {
   int64_t q_row, q_head;
   const void* k;
   const void* v;
-  int64_t kv_block, kv_token, kv_head;
+  int64_t kv_block, kv_token, kv_head;  // elements
   const int32_t* tables;
   int64_t table_stride, width;
   const int32_t* lens;
@@ -91,26 +104,25 @@ struct PrefillArgs {
   int num_seqs, hq, hkv;
   int64_t num_blocks;
   int total_items;  // grid work items actually launched
-  float qscale;     // scale * log2(e)
+  float qscale;     // |scale| * log2(e)
+  uint32_t q_sign;  // 0x80008000 negates q (a negative scale), else 0
 };
 
 template <typename T> struct MfmaOps;
 template <> struct MfmaOps<bf16> {
   using V8 = bf16x8;
   __device__ static f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
-  __device__ static uint32_t pack2(float x, float y) { return f32_to_bf16_bits(x) | (f32_to_bf16_bits(y) << 16); }
-  __device__ static void store4(void* p, const float* x) {
-    u32x2 w = {pack2(x[0], x[1]), pack2(x[2], x[3])};
-    *reinterpret_cast<u32x2*>(p) = w;
+  __device__ static uint32_t pack2(float x, float y) {
+    const bf16x2 r = {static_cast<__bf16>(x), static_cast<__bf16>(y)};  // v_cvt_pk_bf16_f32, RNE
+    return __builtin_bit_cast(uint32_t, r);
   }
 };
 template <> struct MfmaOps<f16> {
   using V8 = f16x8;
   __device__ static f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
-  __device__ static uint32_t pack2(float x, float y) { return f16_bits(x) | (f16_bits(y) << 16); }
-  __device__ static void store4(void* p, const float* x) {
-    u32x2 w = {pack2(x[0], x[1]), pack2(x[2], x[3])};
-    *reinterpret_cast<u32x2*>(p) = w;
+  __device__ static uint32_t pack2(float x, float y) {
+    const f16x2 r = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
+    return __builtin_bit_cast(uint32_t, r);
   }
 };
 
@@ -119,20 +131,36 @@ __device__ __forceinline__ V8 as_v8(u32x4 x) {
   return __builtin_bit_cast(V8, x);
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16).  In each 16-lane group, lane L
+// supplies the address of 4 consecutive 16-bit elements; lane j receives
+// element j%4 of the chunks supplied by lanes j/4, j/4+4, j/4+8, j/4+12.  With
+// lane L addressing row L/4, column 4(L%4) of a row-major tile, lane j gets
+// rows 0..3 of column j -- four consecutive keys of one V column.
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, x);
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_mfma_kernel(PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   constexpr int KSTEPS = D / 16;  // q.k k-steps
   constexpr int DTILES = D / 32;  // output column tiles
-  constexpr int KROW = D + 8;     // LDS K row stride (elements): 16-byte pad
-  constexpr int VROW = kBN + 4;   // LDS V^T row stride (elements): 8-byte pad
-  constexpr int CHUNKS = D / 8;   // 16-byte chunks per token row
+  // Row strides in elements.  K: a quarter-wave's 16-byte reads of 16 rows
+  // land in distinct bank groups when the stride is an odd multiple of 16
+  // bytes.  V: the transposing read takes 4 rows x 64 bytes per half-wave, so
+  // the stride is 64 (mod 256) bytes.
+  constexpr int KROW = D + 8;
+  constexpr int VROW = D + 32;
+  constexpr int CHUNKS = D / 8;  // 16-byte chunks per token row
   constexpr int TOKENS_PER_PASS = 256 / CHUNKS;
+  constexpr int PAGES_PER_PASS = TOKENS_PER_PASS / kPage;
   constexpr int PASSES = kBN / TOKENS_PER_PASS;
-  static_assert(kBN % TOKENS_PER_PASS == 0, "tile loads");
+  static_assert(kBN % TOKENS_PER_PASS == 0 && TOKENS_PER_PASS % kPage == 0, "tile loads");
+  static_assert(64 % CHUNKS == 0 && (64 / CHUNKS) <= kPage, "a wave's loads stay in one page");
   __shared__ __align__(16) uint16_t k_lds[kBN * KROW];
-  __shared__ __align__(16) uint16_t vt_lds[D * VROW];
+  __shared__ __align__(16) uint16_t v_lds[kBN * VROW];
 
   // XCD-major work mapping: xcd x gets a contiguous run of the work list
   // (gridDim.x is a multiple of kXcds, so this is a bijection).
@@ -161,7 +189,7 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) 
   const int kvh = h / (a.hq / a.hkv);
   const int qt0 = t * kBM;                         // first chunk row of the workgroup
   const int wg_last_row = min(qt0 + kBM, nq) - 1;  // last chunk row of the workgroup
-  const int wg_keys = prefix + wg_last_row + 1;
+  const int wg_keys = prefix + wg_last_row + 1;    // <= len_k, so len_k >= 1 below
   if (wg_keys <= 0) return;
   const int ntiles = (wg_keys + kBN - 1) / kBN;
 
@@ -183,26 +211,47 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) 
     const int r = row0 + min(my_row, nq - 1);
     const T* qrow = static_cast<const T*>(a.q) + r * a.q_row + static_cast<int64_t>(h) * a.q_head;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
+    for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8) ^ a.q_sign;
   }
 
   const int32_t* trow = a.tables + static_cast<int64_t>(seq) * a.table_stride;
-  const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(kvh) * a.kv_head;
-  const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(kvh) * a.kv_head;
+  const char* kbase = static_cast<const char*>(a.k) + static_cast<int64_t>(kvh) * a.kv_head * sizeof(T);
+  const char* vbase = static_cast<const char*>(a.v) + static_cast<int64_t>(kvh) * a.kv_head * sizeof(T);
+  const int64_t block_bytes = a.kv_block * static_cast<int64_t>(sizeof(T));
+  const uint32_t nblocks = static_cast<uint32_t>(a.num_blocks);
   const int ld_tok = tid / CHUNKS;
+  const int ld_page = uniform(ld_tok / kPage);
+  const int ld_slot = ld_tok % kPage;
   const int ld_chunk = tid % CHUNKS;
+  const int last_page = (len_k - 1) / kPage;
+  const int last_slot = (len_k - 1) % kPage;
+  const uint32_t off_full = static_cast<uint32_t>((ld_slot * a.kv_token + ld_chunk * 8) * sizeof(T));
+  const uint32_t off_last = static_cast<uint32_t>((min(ld_slot, last_slot) * a.kv_token + ld_chunk * 8) * sizeof(T));
+  constexpr int kTilesPerChunk = 64 / (kBN / kPage);
+  auto table_chunk = [&](int c) { return trow[min(c * 64 + lane, last_page)]; };
+  int32_t tab_cur = table_chunk(0), tab_next = table_chunk(1);
   u32x4 kreg[PASSES], vreg[PASSES];
   auto load_tile = [&](int j) {
+    if (j % kTilesPerChunk == 0 && j > 0) {
+      tab_cur = tab_next;
+      tab_next = table_chunk(j / kTilesPerChunk + 1);
+    }
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
-      const int tok = min(j * kBN + i * TOKENS_PER_PASS + ld_tok, len_k - 1);
-      int64_t blk = trow[tok / kPage];
-      blk = (blk < 0 || blk >= a.num_blocks) ? 0 : blk;
-      const int64_t off = blk * a.kv_block + static_cast<int64_t>(tok % kPage) * a.kv_token + ld_chunk * 8;
-      kreg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + off));
-      vreg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + off));
+      const int p = j * (kBN / kPage) + i * PAGES_PER_PASS + ld_page;
+      const uint32_t id = static_cast<uint32_t>(__builtin_amdgcn_readlane(tab_cur, p % 64));
+      const int64_t blk = id < nblocks ? id : 0;
+      const uint32_t off = p >= last_page ? off_last : off_full;
+      kreg[i] = *reinterpret_cast<const u32x4*>(kbase + blk * block_bytes + off);
+      vreg[i] = *reinterpret_cast<const u32x4*>(vbase + blk * block_bytes + off);
     }
   };
+
+  // V^T A-operand reads: within k-step ks, lane (dim i, half kh) needs keys
+  // 16ks + 4kh + {0..3} (elements 0-3) and 16ks + 8 + 4kh + {0..3} (4-7) --
+  // the key order of the P^T B operand below.
+  const int grp = lane >> 4, gl = lane & 15;
+  const int tr_off = (4 * (grp >> 1) + (gl >> 2)) * VROW + 16 * (grp & 1) + 4 * (gl & 3);
 
   f32x16 acc_o[DTILES];
 #pragma unroll
@@ -216,11 +265,7 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) 
     for (int i = 0; i < PASSES; ++i) {
       const int tok = i * TOKENS_PER_PASS + ld_tok;
       *reinterpret_cast<u32x4*>(&k_lds[tok * KROW + ld_chunk * 8]) = kreg[i];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt_lds[(ld_chunk * 8 + 2 * e) * VROW + tok] = static_cast<uint16_t>(vreg[i][e] & 0xffffu);
-        vt_lds[(ld_chunk * 8 + 2 * e + 1) * VROW + tok] = static_cast<uint16_t>(vreg[i][e] >> 16);
-      }
+      *reinterpret_cast<u32x4*>(&v_lds[tok * VROW + ld_chunk * 8]) = vreg[i];
     }
     __syncthreads();
     if (j + 1 < ntiles) load_tile(j + 1);
@@ -239,39 +284,47 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) 
       }
       sacc[hh] = c;
     }
-    // Scale, mask (diagonal tiles only), online softmax for query my_row.
-    const bool needs_mask = key0 + kBN - 1 > prefix + wave_row0 || !row_valid;
     float tmax = -INFINITY;
+    if (uniform(key0 + kBN - 1 > prefix + wave_row0 || wave_row0 + 31 >= nq)) {
+      const int lim = row_valid ? my_key_limit - key0 - 4 * half : -1;
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
+      for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = sacc[hh][r] * a.qscale;
-        if (needs_mask) {
-          const int key = key0 + hh * 32 + (r / 4) * 8 + half * 4 + (r % 4);
-          if (key > my_key_limit || !row_valid) x = -INFINITY;
+        for (int r = 0; r < 16; ++r) {
+          const float x = (hh * 32 + (r / 4) * 8 + (r % 4) > lim) ? -INFINITY : sacc[hh][r];
+          sacc[hh][r] = x;
+          tmax = fmaxf(tmax, x);
         }
-        sacc[hh][r] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = fmaxf(tmax, xor_lane(tmax, 32));
-    const float mn = fmaxf(m, tmax);
-    const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[hh][r]);
+    }
+    tmax = fmaxf(tmax, xor_lane(tmax, 32)) * a.qscale;
+    if (__builtin_amdgcn_ballot_w64(tmax > m + kRescale)) {
+      const float mn = fmaxf(m, tmax);
+      const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+      lsum *= corr;
+#pragma unroll
+      for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
+      m = mn;
+    }
+    // p = 2^(s * scale * log2(e) - m); a lane that has seen no key yet has
+    // only -inf scores, which give 0 against any finite offset.
+    const float mb = (m == -INFINITY) ? 0.f : m;
     float psum = 0.f;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = (sacc[hh][r] == -INFINITY) ? 0.f : fast_exp2(sacc[hh][r] - mn);
+        const float p = fast_exp2(fmaf(sacc[hh][r], a.qscale, -mb));
         sacc[hh][r] = p;
         psum += p;
       }
-    lsum = lsum * corr + psum;
-    m = mn;
-#pragma unroll
-    for (int c = 0; c < DTILES; ++c)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
+    lsum += psum;
 
     // O^T += V^T P^T over the tile's four 16-key k-steps.
 #pragma unroll
@@ -282,9 +335,9 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) 
       for (int e = 0; e < 4; ++e) pb[e] = Ops::pack2(sacc[hh][base + 2 * e], sacc[hh][base + 2 * e + 1]);
 #pragma unroll
       for (int c = 0; c < DTILES; ++c) {
-        const uint16_t* vrow = &vt_lds[(c * 32 + col) * VROW + ks * 16 + half * 4];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+        const uint16_t* vp = &v_lds[tr_off + ks * 16 * VROW + c * 32];
+        const u32x2 lo = lds_read_tr(vp);
+        const u32x2 hi = lds_read_tr(vp + 8 * VROW);
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
         acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
       }
@@ -299,10 +352,9 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma_kernel(PrefillArgs a) 
   for (int c = 0; c < DTILES; ++c)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      float x[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = acc_o[c][g * 4 + e] * inv;
-      Ops::store4(orow + c * 32 + g * 8 + half * 4, x);
+      const u32x2 w2 = {Ops::pack2(acc_o[c][g * 4] * inv, acc_o[c][g * 4 + 1] * inv),
+                        Ops::pack2(acc_o[c][g * 4 + 2] * inv, acc_o[c][g * 4 + 3] * inv)};
+      *reinterpret_cast<u32x2*>(orow + c * 32 + g * 8 + half * 4) = w2;
     }
 }
 
@@ -361,6 +413,8 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     return fail(RLT_EINVAL, "rlt_paged_prefill: query heads must be a positive multiple of KV heads");
   if (head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
     return fail(RLT_EINVAL, "rlt_paged_prefill: head_dim, page_size and num_blocks must be positive");
+  if (!(scale != 0.f) || !std::isfinite(scale))
+    return fail(RLT_EINVAL, "rlt_paged_prefill: scale must be finite and nonzero");
 
   const int esize = dtype_size(dtype);
   const bool mfma_ok = mfma_shape(head_dim, page_size, dtype) && q_strides[2] == 1 && out_strides[2] == 1 && kv_strides[3] == 1 &&
@@ -368,7 +422,8 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
                        stride16(q_strides[0], esize) && stride16(q_strides[1], esize) &&
                        stride16(out_strides[0], esize) && stride16(out_strides[1], esize) &&
                        stride16(kv_strides[0], esize) && stride16(kv_strides[1], esize) &&
-                       stride16(kv_strides[2], esize) && max_table_width > 0 && num_q_heads <= 4096;
+                       stride16(kv_strides[2], esize) && max_table_width > 0 && num_q_heads <= 4096 &&
+                       kv_strides[1] >= 0 && kv_strides[1] * esize * page_size < (int64_t(1) << 31);
   if (mfma_ok) {
     PrefillArgs p{};
     p.q = q;
@@ -391,7 +446,9 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     p.hq = static_cast<int>(num_q_heads);
     p.hkv = static_cast<int>(num_kv_heads);
     p.num_blocks = num_blocks;
-    p.qscale = scale * kLog2eP;
+    // s * scale == (-s) * |scale|: a negative scale negates q exactly (sign bits).
+    p.qscale = std::fabs(scale) * kLog2eP;
+    p.q_sign = scale < 0.f ? 0x80008000u : 0u;
     const int64_t tiles_bound = (total_q + kBM - 1) / kBM + num_seqs;
     const int64_t items = tiles_bound * num_q_heads;
     if (items > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_paged_prefill: too many query tiles");
