@@ -79,7 +79,6 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kPage = 16;
-constexpr int kXcds = 8;
 constexpr float kLog2eP = 1.4426950408889634f;
 // A row's running maximum is only moved (and its sums rescaled) when a tile's
 // maximum exceeds it by more than this many powers of two; until then the
@@ -103,10 +102,19 @@ struct PrefillArgs {
   int64_t o_row, o_head;
   int num_seqs, hq, hkv;
   int64_t num_blocks;
-  int total_items;  // grid work items actually launched
+  int total_q;      // rows of q / out; cu_seqlens_q entries are clamped to it
+  int ranked;       // work-list mode (see the kernel)
+  int max_qt;       // direct mode: query tiles per sequence bound
   float qscale;     // |scale| * log2(e)
   uint32_t q_sign;  // 0x80008000 negates q (a negative scale), else 0
 };
+
+// Rows [row0, row0 + nq) of sequence s, clamped to [0, total_q] so that an
+// inconsistent cu_seqlens_q cannot index outside q and out.
+__device__ __forceinline__ void seq_rows(const PrefillArgs& a, int s, int& row0, int& nq) {
+  row0 = min(max(a.cu[s], 0), a.total_q);
+  nq = min(max(a.cu[s + 1], row0), a.total_q) - row0;
+}
 
 template <typename T> struct MfmaOps;
 template <> struct MfmaOps<bf16> {
@@ -141,8 +149,21 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, x);
 }
 
+// Work list.  A work item is (sequence, query tile of kBM rows, query head).
+// Ranked mode (few sequences, hq a multiple of the XCD count): every workgroup
+// ranks the sequences by the key tiles of their last query tile, longest
+// first.  Workgroup b runs on XCD b % 8 (the dispatcher's round-robin) and is
+// that XCD's (b / 8)-th item; each XCD's queue walks the ranked sequences, for
+// each its heads h == xcd (mod 8), and for each head the query tiles, last
+// (longest) first.  So the dispatcher hands out the longest items first on
+// every XCD (greedy LPT), and the query tiles that stream one (sequence,
+// head)'s prefix run back to back on one XCD, sharing its L2.  Direct mode:
+// item = (seq * max_qt + t) * hq + head; empty items exit.
+constexpr int kXcds = 8;
+constexpr int kRankSeqs = 512;  // ranked mode: at most this many sequences
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_mfma_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_mfma_kernel(PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   constexpr int KSTEPS = D / 16;  // q.k k-steps
@@ -153,36 +174,83 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // the stride is 64 (mod 256) bytes.
   constexpr int KROW = D + 8;
   constexpr int VROW = D + 32;
+  constexpr int KT = kBN * KROW, VT = kBN * VROW;  // elements per K / V tile
   constexpr int CHUNKS = D / 8;  // 16-byte chunks per token row
   constexpr int TOKENS_PER_PASS = 256 / CHUNKS;
   constexpr int PAGES_PER_PASS = TOKENS_PER_PASS / kPage;
   constexpr int PASSES = kBN / TOKENS_PER_PASS;
+  constexpr int TILES_PER_CHUNK = 64 / (kBN / kPage);  // table entries arrive 64 at a time
+  constexpr int MERGE_FLOATS = 2 + 16 * DTILES;        // m, l, accumulators per lane
   static_assert(kBN % TOKENS_PER_PASS == 0 && TOKENS_PER_PASS % kPage == 0, "tile loads");
   static_assert(64 % CHUNKS == 0 && (64 / CHUNKS) <= kPage, "a wave's loads stay in one page");
-  __shared__ __align__(16) uint16_t k_lds[kBN * KROW];
-  __shared__ __align__(16) uint16_t v_lds[kBN * VROW];
+  static_assert(4 * 64 * MERGE_FLOATS * 4 <= 4 * (KT + VT) * 2, "merge fits in the tile buffers");
+  static_assert(4 * kRankSeqs * 4 <= 4 * (KT + VT) * 2, "ranking fits in the tile buffers");
+  // Two key groups, each with two K and V tile buffers; reused for ranking
+  // before the tile loop and for the key-group merge after it.
+  __shared__ __align__(16) uint16_t lds[4 * (KT + VT)];
 
-  // XCD-major work mapping: xcd x gets a contiguous run of the work list
-  // (gridDim.x is a multiple of kXcds, so this is a bijection).
-  const int per_xcd = gridDim.x / kXcds;
-  const int w = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (w >= a.total_items) return;
-  // Work list: head-major, then query tiles of sequences in order.
-  int tiles_total = 0;
-  for (int s = 0; s < a.num_seqs; ++s) tiles_total += (a.cu[s + 1] - a.cu[s] + kBM - 1) / kBM;
-  if (tiles_total == 0) return;
-  const int h = w / tiles_total;
-  int t = w - h * tiles_total;
-  if (h >= a.hq) return;
-  int seq = 0;
-  for (; seq < a.num_seqs; ++seq) {
-    const int n = (a.cu[seq + 1] - a.cu[seq] + kBM - 1) / kBM;
-    if (t < n) break;
-    t -= n;
+  const int tid = threadIdx.x;
+  int seq, t, h;
+  if (a.ranked) {
+    int* s_qt = reinterpret_cast<int*>(lds);  // [kRankSeqs] query tiles per sequence
+    int* s_cost = s_qt + kRankSeqs;            // key tiles of its last query tile
+    int* s_order = s_cost + kRankSeqs;         // sequences, longest first
+    int* s_scan = s_order + kRankSeqs;         // query tiles of the ranked sequences, prefix sums
+    const int ns = a.num_seqs;
+    if (tid < ns) {
+      int r0, nq_s;
+      seq_rows(a, tid, r0, nq_s);
+      const int keys = static_cast<int>(min<int64_t>(a.lens[tid], a.width * kPage));
+      s_qt[tid] = (nq_s + kBM - 1) / kBM;
+      s_cost[tid] = keys > 0 ? (keys + kBN - 1) / kBN : 0;
+    }
+    __syncthreads();
+    if (tid < ns) {
+      const int c = s_cost[tid];
+      int r = 0;
+      for (int q = 0; q < ns; ++q) {
+        const int cq = s_cost[q];
+        r += (cq > c) || (cq == c && q < tid);
+      }
+      s_order[r] = tid;
+    }
+    __syncthreads();
+    s_scan[tid] = tid < ns ? s_qt[s_order[tid]] : 0;
+    __syncthreads();
+    for (int off = 1; off < kRankSeqs; off <<= 1) {  // inclusive scan
+      const int v = tid >= off ? s_scan[tid - off] : 0;
+      __syncthreads();
+      s_scan[tid] += v;
+      __syncthreads();
+    }
+    // XCD b % 8 owns heads h == b % 8 (mod 8): hpx of them per sequence.
+    const int hpx = a.hq / kXcds;
+    const int xcd = static_cast<int>(blockIdx.x) % kXcds;
+    const int pos = static_cast<int>(blockIdx.x) / kXcds;
+    // Ranked sequence r covers positions [hpx * scan[r-1], hpx * scan[r]).
+    int lo = 0, hi = ns;  // first r with hpx * scan[r] > pos
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (hpx * s_scan[mid] > pos) hi = mid;
+      else lo = mid + 1;
+    }
+    if (lo >= ns) return;
+    seq = s_order[lo];
+    const int qt = s_qt[seq];
+    const int local = pos - hpx * (lo > 0 ? s_scan[lo - 1] : 0);
+    h = xcd + kXcds * (local / qt);
+    t = qt - 1 - local % qt;
+    __syncthreads();  // ranking arrays are dead before the tiles reuse them
+  } else {
+    const int w = blockIdx.x;
+    h = w % a.hq;
+    seq = w / a.hq / a.max_qt;
+    t = w / a.hq % a.max_qt;
+    if (seq >= a.num_seqs) return;
   }
-  if (seq == a.num_seqs) return;
-  const int row0 = a.cu[seq];
-  const int nq = a.cu[seq + 1] - row0;
+  int row0, nq;
+  seq_rows(a, seq, row0, nq);
+  if (t * kBM >= nq) return;
   const int64_t max_len = a.width * kPage;
   const int len_k = static_cast<int>(min<int64_t>(a.lens[seq], max_len));
   const int prefix = len_k - nq;
@@ -193,17 +261,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   if (wg_keys <= 0) return;
   const int ntiles = (wg_keys + kBN - 1) / kBN;
 
-  const int tid = threadIdx.x;
+  // Waves 0-3 take key tiles 0, 2, 4, ...; waves 4-7 tiles 1, 3, 5, ...; wave
+  // w and w + 4 own the same 32 query rows and merge at the end.
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int kg = wave >> 2;   // key group
+  const int qw = wave & 3;    // query wave within the group
+  const int gtid = tid & 255; // thread within the key group
   const int half = lane >> 5;
   const int col = lane & 31;
-  const int wave_row0 = qt0 + wave * 32;  // chunk row of the wave's column 0
+  const int wave_row0 = qt0 + qw * 32;  // chunk row of the wave's column 0
   const bool wave_live = wave_row0 < nq;
   const int wave_last_key = prefix + min(wave_row0 + 31, nq - 1);
   const int my_row = wave_row0 + col;
   const bool row_valid = my_row < nq;
   const int my_key_limit = prefix + my_row;  // last visible key of this lane's query
+  uint16_t* const group_lds = lds + kg * 2 * (KT + VT);  // buffer b: K at b*(KT+VT), V after it
 
   // Q^T B-operands: lane holds dims [ks*16 + half*8, +8) of query my_row.
   u32x4 qb[KSTEPS];
@@ -214,27 +287,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8) ^ a.q_sign;
   }
 
+  // Tile loads: pass i of tile j reads page 4j + i*PAGES_PER_PASS + ld_page,
+  // the same page for the whole wave, so its table entry and base address are
+  // scalar and each lane adds a 32-bit offset.  Table entries arrive 64 at a
+  // time (one per lane, a chunk ahead of use) and are picked with readlane.
+  // Slots past the sequence's last key re-read its last key (masked, but
+  // finite: no unwritten slot is read); out-of-range ids read block 0.
   const int32_t* trow = a.tables + static_cast<int64_t>(seq) * a.table_stride;
   const char* kbase = static_cast<const char*>(a.k) + static_cast<int64_t>(kvh) * a.kv_head * sizeof(T);
   const char* vbase = static_cast<const char*>(a.v) + static_cast<int64_t>(kvh) * a.kv_head * sizeof(T);
   const int64_t block_bytes = a.kv_block * static_cast<int64_t>(sizeof(T));
   const uint32_t nblocks = static_cast<uint32_t>(a.num_blocks);
-  const int ld_tok = tid / CHUNKS;
+  const int ld_tok = gtid / CHUNKS;
   const int ld_page = uniform(ld_tok / kPage);
   const int ld_slot = ld_tok % kPage;
-  const int ld_chunk = tid % CHUNKS;
+  const int ld_chunk = gtid % CHUNKS;
   const int last_page = (len_k - 1) / kPage;
   const int last_slot = (len_k - 1) % kPage;
   const uint32_t off_full = static_cast<uint32_t>((ld_slot * a.kv_token + ld_chunk * 8) * sizeof(T));
   const uint32_t off_last = static_cast<uint32_t>((min(ld_slot, last_slot) * a.kv_token + ld_chunk * 8) * sizeof(T));
-  constexpr int kTilesPerChunk = 64 / (kBN / kPage);
   auto table_chunk = [&](int c) { return trow[min(c * 64 + lane, last_page)]; };
   int32_t tab_cur = table_chunk(0), tab_next = table_chunk(1);
   u32x4 kreg[PASSES], vreg[PASSES];
+  // Tiles of a key group arrive 2 apart: the group's first tile of chunk c
+  // is 16c + kg.
   auto load_tile = [&](int j) {
-    if (j % kTilesPerChunk == 0 && j > 0) {
+    if (j % TILES_PER_CHUNK == kg && j >= TILES_PER_CHUNK) {
       tab_cur = tab_next;
-      tab_next = table_chunk(j / kTilesPerChunk + 1);
+      tab_next = table_chunk(j / TILES_PER_CHUNK + 1);
     }
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
@@ -258,20 +338,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
   float m = -INFINITY, lsum = 0.f;
 
-  load_tile(0);
-  for (int j = 0; j < ntiles; ++j) {
-    __syncthreads();  // everyone is done reading the previous tile
+  // Per key group, iteration it computes tile j = 2it + kg from buffer it&1
+  // while tile j+2 waits in registers; tile j+2 then goes to the other buffer
+  // (whose tile every wave finished before the previous barrier), and one
+  // barrier per tile publishes it.
+  auto store_tile = [&](int b) {
+    uint16_t* kb = group_lds + b * (KT + VT);
+    uint16_t* vb = kb + KT;
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int tok = i * TOKENS_PER_PASS + ld_tok;
-      *reinterpret_cast<u32x4*>(&k_lds[tok * KROW + ld_chunk * 8]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&v_lds[tok * VROW + ld_chunk * 8]) = vreg[i];
+      *reinterpret_cast<u32x4*>(&kb[tok * KROW + ld_chunk * 8]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&vb[tok * VROW + ld_chunk * 8]) = vreg[i];
     }
-    __syncthreads();
-    if (j + 1 < ntiles) load_tile(j + 1);
+  };
+  if (kg < ntiles) {
+    load_tile(kg);
+    store_tile(0);
+  }
+  if (kg + 2 < ntiles) load_tile(kg + 2);
+  __syncthreads();
+  const int niter = (ntiles + 1) / 2;
+  for (int it = 0; it < niter; ++it) {
+    const int j = 2 * it + kg;
+    const uint16_t* k_lds = group_lds + (it & 1) * (KT + VT);
+    const uint16_t* v_lds = k_lds + KT;
     const int key0 = j * kBN;
-    if (!wave_live || key0 > wave_last_key) continue;
-
+    if (j < ntiles && wave_live && key0 <= wave_last_key) {
     // S^T = K Q^T for the tile's two 32-key halves.
     f32x16 sacc[2];
 #pragma unroll
@@ -284,6 +377,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
       sacc[hh] = c;
     }
+    // Mask (diagonal tiles and the chunk's last rows only) and the tile
+    // maximum of this lane's query.  Element r of half hh holds key
+    // key0 + 32hh + 8(r/4) + 4half + r%4.
     float tmax = -INFINITY;
     if (uniform(key0 + kBN - 1 > prefix + wave_row0 || wave_row0 + 31 >= nq)) {
       const int lim = row_valid ? my_key_limit - key0 - 4 * half : -1;
@@ -342,6 +438,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
       }
     }
+    }
+    if (j + 2 < ntiles) store_tile((it + 1) & 1);
+    __syncthreads();
+    if (j + 4 < ntiles) load_tile(j + 4);
+  }
+
+  // Merge the key groups: group 1 hands (m, l, acc) to group 0 through LDS,
+  // laid out [query wave][value][lane] (the loop's last barrier ordered every
+  // tile read before these writes).
+  float* xs = reinterpret_cast<float*>(lds) + qw * MERGE_FLOATS * 64 + lane;
+  if (kg == 1) {
+    xs[0] = m;
+    xs[64] = lsum;
+#pragma unroll
+    for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xs[(2 + c * 16 + r) * 64] = acc_o[c][r];
+  }
+  __syncthreads();
+  if (kg == 1) return;
+  {
+    const float m1 = xs[0];
+    const float mm = fmaxf(m, m1);
+    const float c0 = (m == -INFINITY) ? 0.f : fast_exp2(m - mm);
+    const float c1 = (m1 == -INFINITY) ? 0.f : fast_exp2(m1 - mm);
+    lsum = lsum * c0 + xs[64] * c1;
+#pragma unroll
+    for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[c][r] = acc_o[c][r] * c0 + xs[(2 + c * 16 + r) * 64] * c1;
   }
 
   const float total = lsum + xor_lane(lsum, 32);
@@ -449,20 +575,26 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     // s * scale == (-s) * |scale|: a negative scale negates q exactly (sign bits).
     p.qscale = std::fabs(scale) * kLog2eP;
     p.q_sign = scale < 0.f ? 0x80008000u : 0u;
-    const int64_t tiles_bound = (total_q + kBM - 1) / kBM + num_seqs;
-    const int64_t items = tiles_bound * num_q_heads;
+    // Ranked mode: each XCD's queue holds hq/8 heads of every (sequence,
+    // query tile) pair, at most ceil(total_q / kBM) + num_seqs of them.
+    const int64_t pairs_bound = (total_q + kBM - 1) / kBM + num_seqs;
+    const int64_t max_qt = (max_seqlen_q + kBM - 1) / kBM;
+    p.total_q = static_cast<int>(total_q);
+    p.ranked = num_seqs <= kRankSeqs && num_q_heads % kXcds == 0;
+    if (!p.ranked && max_seqlen_q <= 0)
+      return fail(RLT_EINVAL, "rlt_paged_prefill: max_seqlen_q must cover the longest chunk");
+    p.max_qt = static_cast<int>(std::min<int64_t>(max_qt, 0x7fffffff));
+    const int64_t items = p.ranked ? pairs_bound * num_q_heads : num_seqs * max_qt * num_q_heads;
     if (items > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_paged_prefill: too many query tiles");
-    p.total_items = static_cast<int>(items);
-    // The XCD-major remap is a bijection only on a multiple of 8 workgroups;
-    // the extra ones exit on the item bound.
-    const dim3 grid(static_cast<unsigned>((items + kXcds - 1) / kXcds * kXcds));
+    if (items == 0) return RLT_OK;
+    const dim3 grid(static_cast<unsigned>(items));
     hipStream_t st = as_stream(stream);
     if (dtype == RLT_BFLOAT16) {
-      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
+      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 128>), grid, dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 64>), grid, dim3(512), 0, st, p);
     } else {
-      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 128>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 64>), grid, dim3(256), 0, st, p);
+      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 128>), grid, dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 64>), grid, dim3(512), 0, st, p);
     }
     return check_launch("rlt_paged_prefill");
   }
