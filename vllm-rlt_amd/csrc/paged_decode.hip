@@ -238,8 +238,6 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int t_begin = sp * split_len;
     const int t_end = min(len, t_begin + split_len);
     const int last = t_end - 1;
-    const int first_page = t_begin / P;
-    const int last_rel_page = last / P - first_page;
 
     // q for the G query heads of this kv head, pre-scaled into log2 units.
     float qv[G][EPL];
@@ -268,54 +266,16 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.kv_head;
     const uint32_t tok_stride = static_cast<uint32_t>(a.kv_token);
 
-    // The split's table entries, 64 pages per chunk, one per lane; pages are
-    // picked out with readlane so every K/V load has a scalar page base.
-    int table_chunk = -1;
-    int table_entry = 0;
-    auto tile_pages = [&](int t0, int64_t (&blk)[PPT]) {
-      const int rel0 = (t0 - t_begin) / P;
-      if ((rel0 >> 6) != table_chunk) {
-        table_chunk = rel0 >> 6;
-        const int rel = table_chunk * 64 + lane;
-        table_entry = rel <= last_rel_page ? trow[first_page + rel] : 0;
-      }
-#pragma unroll
-      for (int pg = 0; pg < PPT; ++pg) {
-        const int rel = min(rel0 + pg, last_rel_page);
-        const int64_t b = __builtin_amdgcn_readlane(table_entry, rel & 63);
-        blk[pg] = (b < 0 || b >= a.num_blocks) ? 0 : b;
-      }
-    };
-    auto issue = [&](u32x4 (&dst)[NI], const T* base, const int64_t (&blk)[PPT], int t0) {
-#pragma unroll
-      for (int pg = 0; pg < PPT; ++pg) {
-        const T* page = base + blk[pg] * a.kv_block;
-#pragma unroll
-        for (int i = 0; i < IPP; ++i) {
-          const int tok = min(t0 + pg * P + i * TPI + g, last);
-          const uint32_t off = static_cast<uint32_t>(tok & (P - 1)) * tok_stride + lane_dim;
-          dst[pg * IPP + i] = load_page(reinterpret_cast<const u32x4*>(page + off));
-        }
-      }
-    };
-
-    // Software pipeline: K(t+1) is issued right after the scores of tile t
-    // and V(t+1) right after its value accumulation, so a wave always has
-    // the next tile's loads in flight while it computes, in the same
-    // registers.
-    u32x4 kp[NI], vp[NI];
-    int64_t blk[PPT];
-    tile_pages(t_begin, blk);
-    issue(kp, kbase, blk, t_begin);
-    issue(vp, vbase, blk, t_begin);
-    for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
-      const int t1 = t0 + TILE;
-      const bool more = t1 < t_end;
-      float sc[G][NI];
+    // Loads of tile t + 1 are issued while tile t computes: K(t+1) after the
+    // scores of tile t, V(t+1) after its value accumulation.  The loop body
+    // holds no conditional load (table entries are fetched per 64-page chunk
+    // before its tiles, and the chunk's last tile is peeled), so the compiler
+    // waits only for the tile being consumed and never drains the pipeline.
+    auto scores = [&](const u32x4 (&kt)[NI], int t0, float (&sc)[G][NI]) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         float x[EPL];
-        PK::unpack(kp[i], x);
+        PK::unpack(kt[i], x);
         const bool valid = t0 + i * TPI + g <= last;
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -326,12 +286,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
           sc[j][i] = valid ? dot : -INFINITY;
         }
       }
-      int64_t next_blk[PPT];
-      if (more) {
-        tile_pages(t1, next_blk);
-        issue(kp, kbase, next_blk, t1);
-      }
-
+    };
+    auto accumulate = [&](const u32x4 (&vt)[NI], int t0, const float (&sc)[G][NI]) {
       float p[G][NI];
 #pragma unroll
       for (int j = 0; j < G; ++j) {
@@ -355,13 +311,63 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         float y[EPL];
-        PK::unpack(vp[i], y);
+        PK::unpack(vt[i], y);
 #pragma unroll
         for (int j = 0; j < G; ++j)
 #pragma unroll
           for (int e = 0; e < EPL; ++e) acc[j][e] = fmaf(p[j][i], y[e], acc[j][e]);
       }
-      if (more) issue(vp, vbase, next_blk, t1);
+    };
+
+    constexpr int kChunkTokens = 64 * P;  // one table entry per lane
+    for (int c0 = t_begin; c0 < t_end; c0 += kChunkTokens) {
+      const int c1 = min(t_end, c0 + kChunkTokens);
+      const int chunk_page = c0 / P;
+      const int chunk_last = (c1 - 1) / P - chunk_page;  // <= 63
+      const int table_entry = lane <= chunk_last ? trow[chunk_page + lane] : 0;
+      auto tile_pages = [&](int t0, int64_t (&blk)[PPT]) {
+        const int rel0 = (t0 - c0) / P;
+#pragma unroll
+        for (int pg = 0; pg < PPT; ++pg) {
+          const int64_t b = __builtin_amdgcn_readlane(table_entry, min(rel0 + pg, chunk_last));
+          blk[pg] = (b < 0 || b >= a.num_blocks) ? 0 : b;
+        }
+      };
+      auto issue = [&](u32x4 (&dst)[NI], const T* base, const int64_t (&blk)[PPT], int t0) {
+#pragma unroll
+        for (int pg = 0; pg < PPT; ++pg) {
+          const T* page = base + blk[pg] * a.kv_block;
+#pragma unroll
+          for (int i = 0; i < IPP; ++i) {
+            const int tok = min(t0 + pg * P + i * TPI + g, last);
+            const uint32_t off = static_cast<uint32_t>(tok & (P - 1)) * tok_stride + lane_dim;
+            dst[pg * IPP + i] = load_page(reinterpret_cast<const u32x4*>(page + off));
+          }
+        }
+      };
+      const int ntiles = (c1 - c0 + TILE - 1) / TILE;
+      u32x4 kp[NI], vp[NI];
+      int64_t blk[PPT];
+      // sched_barrier keeps every K load of a tile ahead of its V loads in
+      // issue order, so waiting for K never waits for V.
+      tile_pages(c0, blk);
+      issue(kp, kbase, blk, c0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(vp, vbase, blk, c0);
+      int t0 = c0;
+      for (int it = 1; it < ntiles; ++it, t0 += TILE) {
+        float sc[G][NI];
+        scores(kp, t0, sc);
+        tile_pages(t0 + TILE, blk);
+        issue(kp, kbase, blk, t0 + TILE);
+        __builtin_amdgcn_sched_barrier(0);
+        accumulate(vp, t0, sc);
+        issue(vp, vbase, blk, t0 + TILE);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      float sc[G][NI];
+      scores(kp, t0, sc);
+      accumulate(vp, t0, sc);
     }
 
     // Merge the token groups (lanes that share s).
