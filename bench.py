@@ -78,7 +78,7 @@ def calibrate_counters(device):
 
 
 def profiled_traffic(workload):
-    """HBM bytes per decode launch recorded by the committed rocprofv3 --pmc summary, if any.
+    """HBM bytes per launch of the workload's kernel from the committed rocprofv3 --pmc summary, if any.
 
     The summary carries a line `traffic_bytes_per_launch[<workload>] = <bytes>`
     computed from FETCH_SIZE and WRITE_SIZE scaled by the calibration copy.
@@ -436,7 +436,7 @@ def run_prefill(args, device):
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(launch_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic("ouro-prefill"),
             "avg_launch_ms": round(launch_ms, 5),
             "algorithmic_flops_per_launch": int(flops / (LOOPS * LAYERS)),
         },
