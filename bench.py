@@ -40,10 +40,23 @@ HBM_PEAK_GBS = 8000.0
 LAYERS, HQ, HKV, HEAD_DIM, PAGE, LOOPS = 24, 16, 16, 128, 16, 4
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Decode workloads.  ctx: initial context lengths U[lo, hi]; planes: KV storage
+# planes (LAST-EXITED = one per loop depth, SHARED = 1); depth_probs: exit-depth
+# distribution (None: every step each request sits at a depth drawn uniformly);
+# refill: requests run their loops to the exit depth, finish after a few tokens
+# and are replaced, their pages freed and handed out again in random order;
+# prefix: tokens of a common prefix whose pages are aliased in every table.
 WORKLOADS = {
-    "ouro-last-exited": dict(batch=64, ctx=(512, 4096), planes=LOOPS, depth_probs=None),
-    "ouro-shared": dict(batch=256, ctx=(1024, 8192), planes=1, depth_probs=(0.1, 0.2, 0.3, 0.4)),
+    "ouro-last-exited": dict(batch=64, ctx=(512, 4096), planes=LOOPS, depth_probs=None, refill=False, prefix=0),
+    "ouro-shared": dict(
+        batch=256, ctx=(1024, 8192), planes=1, depth_probs=(0.1, 0.2, 0.3, 0.4), refill=True, prefix=0
+    ),
+    "ouro-prefix-stress": dict(
+        batch=64, ctx=(16384, 32768), planes=1, depth_probs=None, refill=False, prefix=8192
+    ),
 }
+# SHARED refill: a request finishes after U{1..8} generated tokens.
+REFILL_TOKENS = (1, 8)
 # Chunked prefill: 8 sequences x 512 new tokens over prefixes U[0, 16384], the
 # full 4-loop prefill (4 depths x 24 layers of append + packed attention).
 PREFILL = dict(seqs=8, chunk=512, prefix=(0, 16384))
@@ -93,6 +106,128 @@ def profiled_traffic(workload):
     return None
 
 
+def describe(name):
+    cfg = WORKLOADS[name]
+    lo, hi = cfg["ctx"]
+    text = (
+        f"{name}: Ouro-1.4B decode, 24 layers, {cfg['planes']} KV plane(s), 16/16 heads, head_dim 128, page 16, "
+        f"bf16, batch {cfg['batch']}, contexts U[{lo},{hi}]"
+    )
+    if cfg["refill"]:
+        text += (
+            f", exit depth P(1..4)={list(cfg['depth_probs'])} with loops run to the exit depth, requests "
+            f"replaced after U{{{REFILL_TOKENS[0]}..{REFILL_TOKENS[1]}}} tokens, freed pages reused in random order"
+        )
+    elif cfg["planes"] > 1:
+        text += ", each step every request at a depth drawn from U{1..4}"
+    if cfg["prefix"]:
+        text += f", a {cfg['prefix']}-token prefix aliased read-only in every table"
+    return text + "; loop-step = metadata build + 24 x (KV append + decode)"
+
+
+def make_schedule(name, total_steps, seed):
+    """Host-side page tables and per-step (slot, plane, position) descriptors of a decode workload.
+
+    Returns (descriptors [steps, batch, 3] int64, tables [slots, planes, width]
+    int32, num_blocks, contexts, shared_pages).  Without refill, every request
+    keeps one slot, appends at context + step, and its table covers every
+    position the run touches.  With refill (SHARED), a request runs loops
+    0 .. exit-1 on one position, then moves to the next; after its generated
+    tokens it leaves, its pages return to the free list, and a new request
+    with a fresh context takes a new slot, drawing pages at random positions
+    of the free list.
+    """
+    import random
+
+    cfg = WORKLOADS[name]
+    batch, planes = cfg["batch"], cfg["planes"]
+    lo, hi = cfg["ctx"]
+    g = torch.Generator().manual_seed(seed)
+    contexts = torch.randint(lo, hi + 1, (batch,), generator=g)
+    if not cfg["refill"]:
+        prefix_pages = cfg["prefix"] // PAGE
+        pages = (contexts + total_steps + PAGE - 1) // PAGE
+        width = int(pages.max())
+        own = [int(n) - prefix_pages for n in pages]
+        num_blocks = prefix_pages + sum(own) * planes
+        perm = torch.randperm(num_blocks, generator=g).to(torch.int32)
+        shared = perm[:prefix_pages]
+        used = prefix_pages
+        tables = torch.zeros(batch, planes, width, dtype=torch.int32)
+        for r in range(batch):
+            for plane in range(planes):
+                tables[r, plane, :prefix_pages] = shared
+                tables[r, plane, prefix_pages : prefix_pages + own[r]] = perm[used : used + own[r]]
+                used += own[r]
+        if cfg["depth_probs"] is None:
+            depths = torch.randint(0, LOOPS, (total_steps, batch), generator=g)
+        else:
+            probs = torch.tensor(cfg["depth_probs"])
+            depths = torch.multinomial(probs, total_steps * batch, replacement=True, generator=g)
+            depths = depths.view(total_steps, batch)
+        steps = torch.arange(total_steps)[:, None]
+        desc = torch.stack(
+            [
+                torch.arange(batch).expand(total_steps, -1),
+                depths if planes > 1 else torch.zeros_like(depths),
+                contexts[None, :] + steps,
+            ],
+            dim=-1,
+        ).to(torch.int64)
+        return desc, tables, num_blocks, contexts, shared.long()
+
+    rng = random.Random(seed)
+    probs = cfg["depth_probs"]
+    tok_lo, tok_hi = REFILL_TOKENS
+
+    def draw_exit():
+        return rng.choices(range(1, LOOPS + 1), weights=probs)[0]
+
+    def need(ctx, gen):
+        return (ctx + gen + PAGE - 1) // PAGE
+
+    gens = [rng.randint(tok_lo, tok_hi) for _ in range(batch)]
+    first = [need(int(contexts[r]), gens[r]) for r in range(batch)]
+    num_blocks = int(sum(first) * 1.02) + 64
+    free = list(range(num_blocks))
+    slot_pages = []
+
+    def admit(ctx, gen):
+        n = need(ctx, gen)
+        got = []
+        for _ in range(n):  # a random free page, O(1) per page
+            i = rng.randrange(len(free))
+            free[i], free[-1] = free[-1], free[i]
+            got.append(free.pop())
+        slot_pages.append(got)
+        return len(slot_pages) - 1
+
+    state = []  # [slot, position, depth, exit, tokens left]
+    for r in range(batch):
+        state.append([admit(int(contexts[r]), gens[r]), int(contexts[r]), 0, draw_exit(), gens[r]])
+    desc = torch.empty(total_steps, batch, 3, dtype=torch.int64)
+    for step in range(total_steps):
+        for r, st in enumerate(state):
+            desc[step, r, 0], desc[step, r, 1], desc[step, r, 2] = st[0], 0, st[1]
+        for st in state:
+            st[2] += 1
+            if st[2] < st[3]:
+                continue
+            st[1], st[2], st[3], st[4] = st[1] + 1, 0, draw_exit(), st[4] - 1
+            if st[4] > 0:
+                continue
+            free.extend(slot_pages[st[0]])
+            gen = rng.randint(tok_lo, tok_hi)
+            ctx = rng.randint(lo, hi)
+            ctx = max(1, min(ctx, len(free) * PAGE - gen))
+            st[:] = [admit(ctx, gen), ctx, 0, draw_exit(), gen]
+    width = max(len(pg) for pg in slot_pages)
+    tables = torch.zeros(len(slot_pages), 1, width, dtype=torch.int32)
+    for slot, pg in enumerate(slot_pages):
+        tables[slot, 0, : len(pg)] = torch.tensor(pg, dtype=torch.int32)
+    return desc, tables, num_blocks, contexts, torch.empty(0, dtype=torch.int64)
+
+
 class Workload:
     """Device-resident pool, page tables, per-step descriptors and per-layer inputs."""
 
@@ -102,42 +237,13 @@ class Workload:
         self.batch = cfg["batch"]
         self.planes = cfg["planes"]
         self.device = device
-        g = torch.Generator().manual_seed(seed)
-        lo, hi = cfg["ctx"]
-        self.contexts = torch.randint(lo, hi + 1, (self.batch,), generator=g)
-        # Capacity for every position the run will touch.
-        capacity = self.contexts + total_steps
-        pages = (capacity + PAGE - 1) // PAGE
-        self.width = int(pages.max())
-        self.num_blocks = int(pages.sum()) * self.planes
-        perm = torch.randperm(self.num_blocks, generator=g)
-        tables = torch.zeros(self.batch, self.planes, self.width, dtype=torch.int32)
-        used = 0
-        for r in range(self.batch):
-            for plane in range(self.planes):
-                n = int(pages[r])
-                tables[r, plane, :n] = perm[used : used + n].to(torch.int32)
-                used += n
+        desc, tables, self.num_blocks, self.contexts, self.shared_pages = make_schedule(name, total_steps, seed)
+        self.width = tables.shape[2]
         self.tables_host = tables
         self.tables = tables.to(device)
-        # Per-step (slot, depth, position) descriptors.
-        if cfg["depth_probs"] is None:
-            depths = torch.randint(0, LOOPS, (total_steps, self.batch), generator=g)
-        else:
-            probs = torch.tensor(cfg["depth_probs"])
-            depths = torch.multinomial(probs, total_steps * self.batch, replacement=True, generator=g)
-            depths = depths.view(total_steps, self.batch)
-        steps = torch.arange(total_steps)[:, None]
-        desc = torch.stack(
-            [
-                torch.arange(self.batch).expand(total_steps, -1),
-                depths if self.planes > 1 else torch.zeros_like(depths),
-                self.contexts[None, :] + steps,
-            ],
-            dim=-1,
-        ).to(torch.int64)
-        self.depths = depths
+        self.descriptors_host = desc
         self.descriptors = desc.to(device)  # [steps, batch, 3]
+        self.prefix_tokens = cfg["prefix"]
         # Pool [blocks, layers, page, kv_heads, head_dim], filled with N(0,1) bf16.
         shape = (self.num_blocks, LAYERS, PAGE, HKV, HEAD_DIM)
         self.key_cache = torch.empty(shape, dtype=torch.bfloat16, device=device)
@@ -169,10 +275,21 @@ class Workload:
 
     def lengths_at(self, step):
         """Attention length of every row at a step (context incl. the appended token)."""
-        return (self.contexts + step + 1).tolist()
+        return (self.descriptors_host[step, :, 2] + 1).tolist()
 
     def pool_bytes(self):
         return 2 * self.key_cache.numel() * self.key_cache.element_size()
+
+    def shared_snapshot(self):
+        """Copies of the aliased prefix pages (all layers), to prove they stay read-only."""
+        if self.shared_pages.numel() == 0:
+            return None
+        idx = self.shared_pages.to(self.device)
+        return self.key_cache[idx].clone(), self.value_cache[idx].clone()
+
+    def shared_unchanged(self, snapshot):
+        idx = self.shared_pages.to(self.device)
+        return torch.equal(self.key_cache[idx], snapshot[0]) and torch.equal(self.value_cache[idx], snapshot[1])
 
 
 def build_metadata(w, step):
@@ -200,14 +317,20 @@ def loop_step(w, step):
         layer_step(w, layer)
 
 
-def step_bytes(lengths):
-    """Algorithmic HBM bytes of one loop-step (24 layer-steps) and of one decode launch."""
+def step_bytes(lengths, shared_tokens=0):
+    """Algorithmic HBM bytes of one loop-step (24 layer-steps) and of one decode launch.
+
+    Returns (loop-step bytes, decode-launch bytes, decode-launch unique bytes):
+    the unique figure counts the K/V of `shared_tokens` aliased prefix tokens
+    once per launch instead of once per row that reads them.
+    """
     kv_token = 2 * HKV * HEAD_DIM * 2  # K+V of one token in one layer (8 KiB)
     qo = 2 * HQ * HEAD_DIM * 2  # q read + out write
     new_kv = 2 * HKV * HEAD_DIM * 2
     decode = sum(kv_token * n + qo + 4 * math.ceil(n / PAGE) + 4 for n in lengths)
     append = len(lengths) * (2 * new_kv + 16)  # read new k/v, write the page slots, block+offset
-    return LAYERS * (decode + append), decode
+    unique = decode - kv_token * shared_tokens * (len(lengths) - 1) if shared_tokens else decode
+    return LAYERS * (decode + append), decode, unique
 
 
 def spot_check(w):
@@ -481,6 +604,7 @@ def main():
         flush=True,
     )
 
+    snapshot = w.shared_snapshot()
     # Warmup (also the parity spot check on step 0).
     for step in range(args.warmup):
         loop_step(w, step)
@@ -491,11 +615,12 @@ def main():
 
     # Timed region: exactly `steps` loop-steps.
     total_bytes = 0
-    decode_bytes = []
+    decode_bytes, unique_bytes = [], []
     for step in range(args.warmup, total):
-        b, d = step_bytes(w.lengths_at(step))
+        b, d, u = step_bytes(w.lengths_at(step), w.prefix_tokens)
         total_bytes += b
         decode_bytes.append(d)
+        unique_bytes.append(u)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for step in range(args.warmup, total):
@@ -524,7 +649,15 @@ def main():
     torch.cuda.synchronize()
     decode_ms = statistics.fmean(s.elapsed_time(e) for s, e in pairs)
     decode_avg_bytes = statistics.fmean(decode_bytes)
-    achieved = decode_avg_bytes / (decode_ms * 1e-3) / 1e9
+    unique_avg_bytes = statistics.fmean(unique_bytes)
+    # Aliased prefix pages are read by every row but fetched from HBM about
+    # once per launch: the roofline uses the unique bytes.
+    achieved = unique_avg_bytes / (decode_ms * 1e-3) / 1e9
+    if snapshot is not None:
+        if not w.shared_unchanged(snapshot):
+            raise SystemExit("aliased prefix pages changed during the run")
+        print("[bench] aliased prefix pages unchanged (bitwise)", file=sys.stderr, flush=True)
+        del snapshot
 
     steps_per_s = args.steps / elapsed
     gbs = total_bytes / elapsed / 1e9
@@ -542,9 +675,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.workload}: Ouro-1.4B decode, 24 layers, {w.planes} KV plane(s), 16/16 heads, "
-            f"head_dim 128, page 16, batch {w.batch}, contexts U[{WORKLOADS[args.workload]['ctx'][0]},"
-            f"{WORKLOADS[args.workload]['ctx'][1]}], loop-step = metadata build + 24 x (KV append + decode)",
+            "workload": describe(args.workload),
             "global_batch": w.batch,
             "seq_len": int(w.contexts.float().mean().item()),
             "parallelism": "single-gpu",
@@ -560,9 +691,12 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(args.workload),
             "avg_launch_ms": round(decode_ms, 5),
-            "algorithmic_bytes_per_launch": int(decode_avg_bytes),
+            "algorithmic_bytes_per_launch": int(unique_avg_bytes),
         },
     }
+    if w.prefix_tokens:
+        line["roofline"]["per_request_bytes_per_launch"] = int(decode_avg_bytes)
+        line["roofline"]["per_request_gb_per_s"] = round(decode_avg_bytes / (decode_ms * 1e-3) / 1e9, 1)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(w, total - 1, args.cpu_reps)
