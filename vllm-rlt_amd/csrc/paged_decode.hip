@@ -1,16 +1,19 @@
 // Single-query paged GQA decode attention for gfx950.
 //
 // Work decomposition.  A row's context [0, len) is cut into fixed splits of
-// kSplitTokens tokens (rows longer than kMaxSplits splits use longer splits,
-// rounded to kSplitAlign).  The split plan of a row depends only on that
-// row's length, so a row's output bits never depend on the rest of the batch.
-// One wavefront processes one (row, kv_head, split) item; the four waves of a
-// workgroup are independent workers that walk the compact item list
-// (rows x splits x kv_heads, kv_head innermost so neighbouring waves read
-// neighbouring 256-byte head slices of the same token rows) in grid-stride
-// order.  Each workgroup first builds the exclusive prefix of split counts
-// over rows in LDS, so no host-side length information and no second launch
-// is needed to enumerate the ragged work.
+// kSplitTokens tokens; rows longer than kMaxSplits splits double the split
+// length until kMaxSplits cover them.  The split plan of a row depends only on
+// that row's length, so a row's output bits never depend on the rest of the
+// batch, and rows of similar length cut at the same token offsets.  One
+// wavefront processes one (row, kv_head, split) item.  When the kv head count
+// is a multiple of the workgroup's 4 waves, a workgroup owns one (row, split,
+// block of 4 heads) and workgroups are laid out so that each XCD serves whole
+// (split, head block) groups with all rows of a group back to back: rows whose
+// tables alias the same pages (a shared prefix) read them at the same time
+// through one L2.  Otherwise the four waves of a workgroup walk the compact
+// item list (rows x splits x kv_heads, kv_head innermost) in grid-stride order,
+// after each workgroup builds the exclusive prefix of split counts over rows
+// in LDS; neither schedule needs host-side length information.
 //
 // Inside an item.  Lanes form 64/LPT token groups of LPT lanes; lane (g, s)
 // owns dims [s*EPL, s*EPL+EPL) of tokens g, g+TPI, ... of every tile.  One
@@ -53,12 +56,15 @@ constexpr int kWaves = 4;
 constexpr int kSplitTokens = RLT_DECODE_SPLIT_TOKENS;
 constexpr int kTile = RLT_DECODE_TILE;
 constexpr int kMaxSplits = 64;
-constexpr int kSplitAlign = 64;
 constexpr int kMaxRowsPerLaunch = 8192;
 #ifndef RLT_DECODE_MAX_GRID
 #define RLT_DECODE_MAX_GRID 4096
 #endif
 constexpr int kMaxGrid = RLT_DECODE_MAX_GRID;
+#ifndef RLT_DECODE_XCD_SCHEDULE
+#define RLT_DECODE_XCD_SCHEDULE 1
+#endif
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
 constexpr float kLog2e = 1.4426950408889634f;
 
 __host__ __device__ inline void split_plan(int len, int* split_len, int* nsplit) {
@@ -73,8 +79,11 @@ __host__ __device__ inline void split_plan(int len, int* split_len, int* nsplit)
     *nsplit = n;
     return;
   }
-  int per = (len + kMaxSplits - 1) / kMaxSplits;
-  per = (per + kSplitAlign - 1) / kSplitAlign * kSplitAlign;
+  // Longer rows double the split length until kMaxSplits cover the row, so
+  // rows of similar length cut their contexts at the same token offsets (an
+  // aliased prefix then falls into the same splits of every row).
+  int per = kSplitTokens;
+  while ((len + per - 1) / per > kMaxSplits) per <<= 1;
   *split_len = per;
   *nsplit = (len + per - 1) / per;
 }
@@ -93,6 +102,7 @@ struct DecodeArgs {
   float* ws_acc;  // [rows][hkv][kMaxSplits][G][D]
   float2* ws_ml;  // [rows][hkv][kMaxSplits][G]  (max in log2 units, sum)
   int n_rows, hkv, hq, d, page;
+  int xcd_groups;  // > 0: XCD-affine schedule over this many (split, head block) groups
   int64_t num_blocks;
   int64_t max_len;  // table width * page: lengths are clamped to what the table covers
   float qscale;     // softmax scale * log2(e)
@@ -196,7 +206,7 @@ __device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int la
   }
 }
 
-template <typename T, int D, int G, int P, int TILE>
+template <typename T, int D, int G, int P, int TILE, bool XCD>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   using PK = Packet<T>;
   constexpr int EPL = PK::N;      // elements of one token a lane owns
@@ -206,11 +216,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   constexpr int PPT = TILE / P;   // pages per tile
   constexpr int NI = TILE / TPI;  // load instructions per tile (per tensor)
   static_assert(D % EPL == 0 && 64 % LPT == 0 && LPT >= 1, "head_dim must map onto whole lanes");
-  static_assert(P % TPI == 0 && TILE % P == 0 && kSplitAlign % TILE == 0, "tile geometry");
-
-  extern __shared__ int prefix[];
-  const int total_splits = build_split_prefix(a, prefix);
-  const int total = total_splits * a.hkv;
+  static_assert(P % TPI == 0 && TILE % P == 0 && kSplitTokens % TILE == 0, "tile geometry");
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -218,14 +224,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   const int s = lane % LPT;
   const uint32_t lane_dim = static_cast<uint32_t>(s * EPL);
 
-  for (int item = blockIdx.x * kWaves + wave; item < total; item += gridDim.x * kWaves) {
-    const int qi = item / a.hkv;
-    const int h = item - qi * a.hkv;
-    const int r = uniform(find_row(prefix, a.n_rows, qi));
-    const int sp = uniform(qi - prefix[r]);
-    const int len = uniform(row_length(a, r));
-    int split_len, ns;
-    split_plan(len, &split_len, &ns);
+  // One (row r, kv head h, split sp) item per wave.
+  auto process = [&](const int r, const int h, const int sp, const int len, const int split_len, const int ns) {
     if (len <= 0) {
       if (g == 0) {
         T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h) * G * a.o_head + lane_dim;
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < G; ++j) *reinterpret_cast<u32x4*>(orow + j * a.o_head) = zero;
       }
-      continue;
+      return;
     }
     const int t_begin = sp * split_len;
     const int t_end = min(len, t_begin + split_len);
@@ -414,6 +414,46 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         for (int j = 0; j < G; ++j) a.ws_ml[slot * G + j] = make_float2(m[j], l[j]);
       }
     }
+  };
+
+  if constexpr (XCD) {
+    // XCD-affine schedule: workgroup b runs on XCD b % kXcds (the dispatcher's
+    // round-robin) and owns one (row, split, block of kWaves heads).  Groups
+    // gi = split * head_blocks + block are dealt out in rounds of kXcds; in
+    // round k XCD x serves group k * kXcds + (x - k) mod kXcds, so every XCD
+    // takes early and late splits alike (later splits have fewer rows).  Each
+    // XCD walks its groups in order with all rows of a group back to back, so
+    // rows that alias the same pages in the same split read them together
+    // from one L2.  Items past a row's split count exit at once.
+    const int b = blockIdx.x;
+    const int t = b / kXcds;
+    const int r = t % a.n_rows;
+    const int round = t / a.n_rows;
+    const int gi = kXcds * round + (b % kXcds + kXcds - round % kXcds) % kXcds;
+    if (gi >= a.xcd_groups) return;
+    const int head_blocks = a.hkv / kWaves;
+    const int sp = gi / head_blocks;
+    const int h = (gi - sp * head_blocks) * kWaves + wave;
+    const int len = uniform(row_length(a, r));
+    int split_len, ns;
+    split_plan(len, &split_len, &ns);
+    if (sp < ns) process(r, h, sp, len, split_len, ns);
+  } else {
+    // Packed schedule (any head count): the compact list of rows x splits x
+    // kv heads, kv head innermost, walked in grid-stride order.
+    extern __shared__ int prefix[];
+    const int total_splits = build_split_prefix(a, prefix);
+    const int total = total_splits * a.hkv;
+    for (int item = blockIdx.x * kWaves + wave; item < total; item += gridDim.x * kWaves) {
+      const int qi = item / a.hkv;
+      const int h = item - qi * a.hkv;
+      const int r = uniform(find_row(prefix, a.n_rows, qi));
+      const int sp = uniform(qi - prefix[r]);
+      const int len = uniform(row_length(a, r));
+      int split_len, ns;
+      split_plan(len, &split_len, &ns);
+      process(r, h, sp, len, split_len, ns);
+    }
   }
 }
 
@@ -495,42 +535,47 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
 // Host dispatch.
 using DecodeKernel = void (*)(DecodeArgs);
 
-template <typename T, int D>
+template <typename T, int D, bool XCD>
 DecodeKernel pick_group(int G) {
   switch (G) {
-    case 1: return paged_decode_kernel<T, D, 1, 16, kTile>;
-    case 2: return paged_decode_kernel<T, D, 2, 16, kTile>;
-    case 4: return paged_decode_kernel<T, D, 4, 16, kTile>;
-    case 8: return paged_decode_kernel<T, D, 8, 16, kTile>;
+    case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD>;
+    case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD>;
+    case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD>;
+    case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD>;
     default: return nullptr;
   }
 }
 
+template <typename T, int D>
+DecodeKernel pick_group(int G, bool xcd) {
+  return xcd ? pick_group<T, D, true>(G) : pick_group<T, D, false>(G);
+}
+
 template <typename T>
-DecodeKernel pick_tiled(int d, int G);
+DecodeKernel pick_tiled(int d, int G, bool xcd);
 template <>
-DecodeKernel pick_tiled<bf16>(int d, int G) {
+DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd) {
   switch (d) {
-    case 64: return pick_group<bf16, 64>(G);
-    case 128: return pick_group<bf16, 128>(G);
-    case 256: return pick_group<bf16, 256>(G);
+    case 64: return pick_group<bf16, 64>(G, xcd);
+    case 128: return pick_group<bf16, 128>(G, xcd);
+    case 256: return pick_group<bf16, 256>(G, xcd);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<f16>(int d, int G) {
+DecodeKernel pick_tiled<f16>(int d, int G, bool xcd) {
   switch (d) {
-    case 64: return pick_group<f16, 64>(G);
-    case 128: return pick_group<f16, 128>(G);
-    case 256: return pick_group<f16, 256>(G);
+    case 64: return pick_group<f16, 64>(G, xcd);
+    case 128: return pick_group<f16, 128>(G, xcd);
+    case 256: return pick_group<f16, 256>(G, xcd);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<float>(int d, int G) {
+DecodeKernel pick_tiled<float>(int d, int G, bool xcd) {
   switch (d) {
-    case 64: return pick_group<float, 64>(G);
-    case 128: return pick_group<float, 128>(G);
+    case 64: return pick_group<float, 64>(G, xcd);
+    case 128: return pick_group<float, 128>(G, xcd);
     default: return nullptr;
   }
 }
@@ -547,7 +592,8 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
                          stride16(a.q_head, esize) && stride16(a.o_row, esize) && stride16(a.o_head, esize) &&
                          stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
                          a.kv_token * a.page < (int64_t(1) << 31);
-  if (layout_ok) tiled = pick_tiled<T>(a.d, G);
+  const bool xcd = RLT_DECODE_XCD_SCHEDULE && a.hkv % kWaves == 0;
+  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd);
   if (!tiled) {
     if (a.d > 64 * kGenericMaxPerLane) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: head_dim > 512");
     if (a.hq > 65535) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: too many query heads");
@@ -556,10 +602,19 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   }
   const int64_t max_tokens = max_table_width * a.page;
   const int64_t splits_cap = std::min<int64_t>(kMaxSplits, (max_tokens + kSplitTokens - 1) / kSplitTokens);
-  const int64_t items = static_cast<int64_t>(a.n_rows) * a.hkv * std::max<int64_t>(splits_cap, 1);
-  const int grid = static_cast<int>(std::min<int64_t>(kMaxGrid, (items + kWaves - 1) / kWaves));
-  const size_t lds = static_cast<size_t>(a.n_rows + 1) * sizeof(int);
-  hipLaunchKernelGGL(tiled, dim3(grid), dim3(64 * kWaves), lds, stream, a);
+  if (xcd) {
+    const int64_t groups = std::max<int64_t>(splits_cap, 1) * (a.hkv / kWaves);
+    const int64_t grid = static_cast<int64_t>(kXcds) * a.n_rows * ((groups + kXcds - 1) / kXcds);
+    if (grid > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: too many work items");
+    a.xcd_groups = static_cast<int>(groups);
+    hipLaunchKernelGGL(tiled, dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), 0, stream, a);
+  } else {
+    const int64_t items = static_cast<int64_t>(a.n_rows) * a.hkv * std::max<int64_t>(splits_cap, 1);
+    const int grid = static_cast<int>(std::min<int64_t>(kMaxGrid, (items + kWaves - 1) / kWaves));
+    const size_t lds = static_cast<size_t>(a.n_rows + 1) * sizeof(int);
+    a.xcd_groups = 0;
+    hipLaunchKernelGGL(tiled, dim3(grid), dim3(64 * kWaves), lds, stream, a);
+  }
   if (int rc = check_launch("rlt_paged_decode")) return rc;
   const int merge_grid = (a.n_rows * a.hkv + kWaves - 1) / kWaves;
   hipLaunchKernelGGL(paged_decode_merge_kernel<T>, dim3(merge_grid), dim3(64 * kWaves), 0, stream, a);
