@@ -69,6 +69,35 @@ int rlt_kv_append(void* key_cache, void* value_cache, const int64_t* cache_strid
                   int64_t num_kv_heads, int64_t head_dim, int dtype, void* stream);
 
 /*
+ * Rotary position embedding of q and k fused with the KV append of one layer.
+ * Replaces, per layer, the rotation of Ouro's attention
+ *   q = q * cos + rotate_half(q) * sin;  k = k * cos + rotate_half(k) * sin
+ *     vllm_rlt/models/ouro.py:104-109 (rotate_half at :73-75)
+ * followed by the append of _write_prepared (vllm_rlt/core/kv_cache_manager.py:
+ * 531-532) and its captured form (vllm_rlt/worker/cuda_graph.py:16-20):
+ *   q_out[i] = rot(q[i])                                       for i < n_rows
+ *   key_cache[write_blocks[i], layer, write_offsets[i]] = rot(k[i])  i < n_write
+ *   value_cache[write_blocks[i], layer, write_offsets[i]] = v[i]     i < n_write
+ * rot(x)[j] = x[j] * cos[j] + rotate_half(x)[j] * sin[j], where each product and
+ * the sum round to the storage dtype as the reference's elementwise tensor ops
+ * do, so q_out and the pages are bit-identical to the unfused sequence given
+ * the same cos / sin (the reference computes them once per traversal,
+ * vllm_rlt/models/ouro.py:209-213, and they are inputs here).  q_out may be q.
+ *   q_strides / k_strides / v_strides / q_out_strides[3]: row, head, dim.
+ *   cos_sin_strides[2]: row, dim strides shared by cos and sin ([n_rows, d]).
+ *   head_dim must be even.
+ */
+int rlt_rope_kv_append(void* key_cache, void* value_cache, const int64_t* cache_strides,
+                       const void* q, const int64_t* q_strides, const void* k,
+                       const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                       const void* cos, const void* sin, const int64_t* cos_sin_strides,
+                       void* q_out, const int64_t* q_out_strides,
+                       const int64_t* write_blocks, const int64_t* write_offsets,
+                       int64_t n_rows, int64_t n_write, int64_t layer, int64_t num_layers,
+                       int64_t num_blocks, int64_t page_size, int64_t num_q_heads,
+                       int64_t num_kv_heads, int64_t head_dim, int dtype, void* stream);
+
+/*
  * Workspace bytes rlt_paged_decode needs for n_rows rows.  Depends only on the
  * shape, never on context lengths, so a caller can size it without a sync.
  */

@@ -4,7 +4,7 @@ Run in the build container only (the reference tree is not shipped):
 
     python tests/golden/make_reference_goldens.py /root/reference
 
-Two fixtures pin what the reference's own tests leave open:
+Three fixtures pin what the reference's own tests leave open:
   allocator_trace.json -- exact physical page ids, refcounts and free counts of
       KVCacheManager (vllm_rlt/core/kv_cache_manager.py:137-344) after every
       step of a scripted sequence of allocate / ensure_capacity / free /
@@ -13,6 +13,10 @@ Two fixtures pin what the reference's own tests leave open:
   paged_attention_cpu.npz -- inputs and exact output bits of
       torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36) on
       seeded bf16 / fp16 / fp32 cases.
+  rotary_cpu.npz -- positions, inputs and exact output bits of the
+      reference's rotary embedding (OuroRotaryEmbedding, vllm_rlt/models/
+      ouro.py:39-70) and of the q/k rotation q * cos + _rotate_half(q) * sin
+      (ouro.py:73-75, 108-109) in bf16 / fp16 / fp32.
 The fixture files hold data only (inputs and outputs).
 """
 
@@ -160,13 +164,42 @@ def attention_cases():
     return arrays
 
 
+def rotary_cases():
+    """Reference rotary angles and q/k rotation (vllm_rlt/models/ouro.py:39-75, 104-109)."""
+    from vllm_rlt.models.config import OuroConfig
+    from vllm_rlt.models.ouro import OuroRotaryEmbedding, _rotate_half
+
+    arrays = {}
+    cases = [
+        ("bf16_ouro", torch.bfloat16, OuroConfig(), 16, [0, 1, 2, 15, 16, 511, 4095, 16383, 32767, 65535]),
+        ("fp16_ouro", torch.float16, OuroConfig(), 4, [0, 3, 1000, 40000]),
+        ("fp32_ouro", torch.float32, OuroConfig(), 2, [0, 7, 20000, 65535]),
+        ("bf16_tiny", torch.bfloat16, OuroConfig.tiny(), 4, [0, 1, 5, 127]),
+    ]
+    for name, dtype, config, heads, positions in cases:
+        g = torch.Generator().manual_seed(len(name) * 131 + config.head_dim)
+        rotary = OuroRotaryEmbedding(config)
+        pos = torch.tensor(positions, dtype=torch.int64)
+        x = (torch.randn(len(positions), heads, config.head_dim, generator=g) * 3).to(dtype)
+        cos, sin = rotary(x, pos)  # [N, 1, D] each, in x's dtype
+        out = x * cos + _rotate_half(x) * sin
+        bits = {torch.bfloat16: torch.int16, torch.float16: torch.int16, torch.float32: torch.int32}[dtype]
+        arrays[f"{name}/positions"] = pos.numpy()
+        arrays[f"{name}/theta"] = np.array(config.rope_theta, dtype=np.float64)
+        arrays[f"{name}/dtype"] = np.array(str(dtype).split(".")[-1])
+        for field, t in (("x", x), ("cos", cos[:, 0]), ("sin", sin[:, 0]), ("out", out)):
+            arrays[f"{name}/{field}"] = t.contiguous().view(bits).numpy()
+    return arrays
+
+
 def main():
     reference = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     sys.path.insert(0, reference)
     torch.set_num_threads(1)
     (OUT / "allocator_trace.json").write_text(json.dumps(allocator_trace(), indent=1))
     np.savez_compressed(OUT / "paged_attention_cpu.npz", **attention_cases())
-    print("wrote", OUT / "allocator_trace.json", OUT / "paged_attention_cpu.npz")
+    np.savez_compressed(OUT / "rotary_cpu.npz", **rotary_cases())
+    print("wrote", OUT / "allocator_trace.json", OUT / "paged_attention_cpu.npz", OUT / "rotary_cpu.npz")
 
 
 if __name__ == "__main__":

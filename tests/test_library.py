@@ -60,6 +60,17 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == native.RLT_EWORKSPACE
     with pytest.raises(ValueError, match="workspace"):
         native.check(rc, "rlt_paged_decode")
+    # Fused rotary append: odd head_dim and n_write > n_rows are refused on the host.
+    s3 = native.int64_array([1, 1, 1])
+    s2 = native.int64_array([1, 1])
+    rc = lib.rlt_rope_kv_append(
+        1, 1, strides, 1, s3, 1, s3, 1, s3, 1, 1, s2, 1, s3, 1, 1, 2, 2, 0, 1, 4, 16, 2, 2, 7, 2, None
+    )
+    assert rc == native.RLT_EINVAL and "even" in native.last_error()
+    rc = lib.rlt_rope_kv_append(
+        1, 1, strides, 1, s3, 1, s3, 1, s3, 1, 1, s2, 1, s3, 1, 1, 2, 3, 0, 1, 4, 16, 2, 2, 8, 2, None
+    )
+    assert rc == native.RLT_EINVAL and "n_write" in native.last_error()
     # Exit-copy targets are validated on the host.
     dst = native.int64_array([3])
     rc = lib.rlt_kv_copy_token(1, 1, strides, 3, dst, 1, 0, 1, 8, 4, 1, 8, 2, None)

@@ -157,6 +157,125 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Rotary embedding fused with the append: grid (n_rows).  Row i rotates its q
+// (all rows) and, for i < n_write, writes its rotated k and its v to the slot
+// (write_blocks[i], layer, write_offsets[i]).  The rotation of a head vector x
+// with per-row cos / sin (each D wide) is, for j < D/2 and h = D/2,
+//   out[j]     = R(R(x[j] * cos[j])       + R(-x[j + h] * sin[j]))
+//   out[j + h] = R(R(x[j + h] * cos[j + h]) + R(x[j] * sin[j + h]))
+// where R rounds to the storage type: each product and the sum round exactly
+// where the elementwise tensor ops x * cos + rotate_half(x) * sin do.  One
+// thread owns both halves of its pair, so q_out may alias q.
+struct RopeArgs {
+  void* cache[2];
+  PoolGeom pool;
+  int64_t layer;
+  const void* x[2];  // q, k
+  int64_t x_row[2], x_head[2], x_dim[2];
+  const void* v;
+  int64_t v_row, v_head, v_dim;
+  void* q_out;
+  int64_t qo_row, qo_head, qo_dim;
+  const void* cos;
+  const void* sin;
+  int64_t cs_row, cs_dim;
+  const int64_t* blocks;
+  const int64_t* offsets;
+  int64_t n_write;
+  int hq, hkv, d;
+};
+
+template <typename T> __device__ __forceinline__ float round_to(float x);
+template <> __device__ __forceinline__ float round_to<bf16>(float x) { return __uint_as_float(f32_to_bf16_bits(x) << 16); }
+template <> __device__ __forceinline__ float round_to<f16>(float x) { return static_cast<float>(static_cast<f16>(x)); }
+template <> __device__ __forceinline__ float round_to<float>(float x) { return x; }
+
+// (lo, hi) <- rotated (x_lo, x_hi) with the cos / sin of both halves.
+template <typename T>
+__device__ __forceinline__ void rotate_pair(float x_lo, float x_hi, float c_lo, float c_hi, float s_lo, float s_hi,
+                                            float* lo, float* hi) {
+#pragma clang fp contract(off)
+  *lo = round_to<T>(round_to<T>(x_lo * c_lo) + round_to<T>(-x_hi * s_lo));
+  *hi = round_to<T>(round_to<T>(x_hi * c_hi) + round_to<T>(x_lo * s_hi));
+}
+
+// VEC: every operand has unit dim stride and 16-byte aligned rows, heads and
+// half-vectors, and the pool slab is contiguous; each thread then moves 16-byte
+// packets.  Otherwise one thread per element (pair) with any strides.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThreads) void rope_kv_append_kernel(RopeArgs a) {
+  using PK = Packet<T>;
+  constexpr int EPV = VEC ? PK::N : 1;  // elements per work unit
+  const int64_t row = blockIdx.x;
+  const int half = a.d / 2;
+  const int pair_units = half / EPV;
+  int64_t block = -1, offset = 0;
+  bool write = row < a.n_write;
+  if (write) {
+    block = a.blocks[row];
+    offset = a.offsets[row];
+    write = block >= 0 && block < a.pool.num_blocks && offset >= 0 && offset < a.pool.page;
+  }
+  const T* cs_c = static_cast<const T*>(a.cos) + row * a.cs_row;
+  const T* cs_s = static_cast<const T*>(a.sin) + row * a.cs_row;
+  const int q_units = a.hq * pair_units;
+  const int k_units = write ? a.hkv * pair_units : 0;
+  const int v_units = write ? a.hkv * (a.d / EPV) : 0;
+  const int total = q_units + k_units + v_units;
+  for (int u = threadIdx.x; u < total; u += kThreads) {
+    if (u < q_units + k_units) {
+      const int which = u < q_units ? 0 : 1;
+      const int w = which ? u - q_units : u;
+      const int head = w / pair_units;
+      const int j0 = (w - head * pair_units) * EPV;
+      const T* x = static_cast<const T*>(a.x[which]) + row * a.x_row[which] + head * a.x_head[which];
+      T* dst;
+      int64_t dst_dim;
+      if (which == 0) {
+        dst = static_cast<T*>(a.q_out) + row * a.qo_row + head * a.qo_head;
+        dst_dim = a.qo_dim;
+      } else {
+        dst = static_cast<T*>(a.cache[0]) + slot_offset(a.pool, block, a.layer, offset) + head * a.pool.slab.head_stride;
+        dst_dim = a.pool.slab.dim_stride;
+      }
+      if constexpr (VEC) {
+        float xl[EPV], xh[EPV], cl[EPV], ch[EPV], sl[EPV], sh[EPV], ol[EPV], oh[EPV];
+        PK::unpack(*reinterpret_cast<const u32x4*>(x + j0), xl);
+        PK::unpack(*reinterpret_cast<const u32x4*>(x + half + j0), xh);
+        PK::unpack(*reinterpret_cast<const u32x4*>(cs_c + j0), cl);
+        PK::unpack(*reinterpret_cast<const u32x4*>(cs_c + half + j0), ch);
+        PK::unpack(*reinterpret_cast<const u32x4*>(cs_s + j0), sl);
+        PK::unpack(*reinterpret_cast<const u32x4*>(cs_s + half + j0), sh);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) rotate_pair<T>(xl[e], xh[e], cl[e], ch[e], sl[e], sh[e], &ol[e], &oh[e]);
+        *reinterpret_cast<u32x4*>(dst + j0) = PK::pack(ol);
+        *reinterpret_cast<u32x4*>(dst + half + j0) = PK::pack(oh);
+      } else {
+        const int64_t xd = a.x_dim[which];
+        float lo, hi;
+        rotate_pair<T>(load_elem(x + j0 * xd), load_elem(x + (half + j0) * xd), load_elem(cs_c + j0 * a.cs_dim),
+                       load_elem(cs_c + (half + j0) * a.cs_dim), load_elem(cs_s + j0 * a.cs_dim),
+                       load_elem(cs_s + (half + j0) * a.cs_dim), &lo, &hi);
+        store_elem(dst + j0 * dst_dim, lo);
+        store_elem(dst + (half + j0) * dst_dim, hi);
+      }
+    } else {
+      const int w = u - q_units - k_units;
+      const int units_per_head = a.d / EPV;
+      const int head = w / units_per_head;
+      const int j0 = (w - head * units_per_head) * EPV;
+      const T* src = static_cast<const T*>(a.v) + row * a.v_row + head * a.v_head;
+      T* dst = static_cast<T*>(a.cache[1]) + slot_offset(a.pool, block, a.layer, offset) + head * a.pool.slab.head_stride;
+      if constexpr (VEC) {
+        *reinterpret_cast<u32x4*>(dst + j0) = *reinterpret_cast<const u32x4*>(src + j0);
+      } else {
+        dst[j0 * a.pool.slab.dim_stride] = src[j0 * a.v_dim];  // bitwise copy
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host helpers.
 bool slab_contiguous(SlabGeom s, int d) { return s.dim_stride == 1 && s.head_stride == d; }
 
@@ -239,6 +358,79 @@ extern "C" int rlt_kv_append(void* key_cache, void* value_cache, const int64_t* 
   RLT_DISPATCH_ESIZE(esize, vec, LAUNCH);
 #undef LAUNCH
   return check_launch("rlt_kv_append");
+}
+
+extern "C" int rlt_rope_kv_append(void* key_cache, void* value_cache, const int64_t* cache_strides, const void* q,
+                                  const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                                  const int64_t* v_strides, const void* cos, const void* sin,
+                                  const int64_t* cos_sin_strides, void* q_out, const int64_t* q_out_strides,
+                                  const int64_t* write_blocks, const int64_t* write_offsets, int64_t n_rows,
+                                  int64_t n_write, int64_t layer, int64_t num_layers, int64_t num_blocks,
+                                  int64_t page_size, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                  int dtype, void* stream) {
+  const int esize = dtype_size(dtype);
+  if (!esize) return fail(RLT_EINVAL, "rlt_rope_kv_append: unknown dtype %d", dtype);
+  if (n_rows < 0 || n_write < 0 || n_write > n_rows)
+    return fail(RLT_EINVAL, "rlt_rope_kv_append: need 0 <= n_write <= n_rows");
+  if (int rc = check_heads(num_kv_heads, head_dim)) return rc;
+  if (head_dim % 2) return fail(RLT_EINVAL, "rlt_rope_kv_append: head_dim must be even for split-half rotation");
+  if (num_q_heads <= 0 || num_q_heads * head_dim > (1 << 24))
+    return fail(RLT_EINVAL, "rlt_rope_kv_append: bad num_q_heads");
+  PoolGeom pool;
+  if (int rc = pool_from(cache_strides, num_blocks, num_layers, page_size, &pool)) return rc;
+  if (layer < 0 || layer >= num_layers)
+    return fail(RLT_EINVAL, "rlt_rope_kv_append: layer %lld out of range", (long long)layer);
+  if (n_rows == 0) return RLT_OK;
+  if (!key_cache || !value_cache || !q || !k || !v || !cos || !sin || !q_out || !q_strides || !k_strides ||
+      !v_strides || !cos_sin_strides || !q_out_strides || (n_write > 0 && (!write_blocks || !write_offsets)))
+    return fail(RLT_EINVAL, "rlt_rope_kv_append: NULL pointer argument");
+  if (n_rows > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_rope_kv_append: too many rows");
+  RopeArgs a{};
+  a.cache[0] = key_cache;
+  a.cache[1] = value_cache;
+  a.pool = pool;
+  a.layer = layer;
+  a.x[0] = q;
+  a.x[1] = k;
+  a.x_row[0] = q_strides[0], a.x_head[0] = q_strides[1], a.x_dim[0] = q_strides[2];
+  a.x_row[1] = k_strides[0], a.x_head[1] = k_strides[1], a.x_dim[1] = k_strides[2];
+  a.v = v;
+  a.v_row = v_strides[0], a.v_head = v_strides[1], a.v_dim = v_strides[2];
+  a.q_out = q_out;
+  a.qo_row = q_out_strides[0], a.qo_head = q_out_strides[1], a.qo_dim = q_out_strides[2];
+  a.cos = cos;
+  a.sin = sin;
+  a.cs_row = cos_sin_strides[0], a.cs_dim = cos_sin_strides[1];
+  a.blocks = write_blocks;
+  a.offsets = write_offsets;
+  a.n_write = n_write;
+  a.hq = static_cast<int>(num_q_heads);
+  a.hkv = static_cast<int>(num_kv_heads);
+  a.d = static_cast<int>(head_dim);
+  auto vec_tensor = [&](const void* p, const int64_t* st, int n) {
+    if (!aligned16(p) || st[n - 1] != 1) return false;
+    for (int i = 0; i + 1 < n; ++i)
+      if ((st[i] * esize) % 16) return false;
+    return true;
+  };
+  const bool vec = (head_dim / 2 * esize) % 16 == 0 && pool_vec_ok(pool, key_cache, value_cache, a.hkv, a.d, esize) &&
+                   vec_tensor(q, q_strides, 3) && vec_tensor(k, k_strides, 3) && vec_tensor(v, v_strides, 3) &&
+                   vec_tensor(q_out, q_out_strides, 3) && vec_tensor(cos, cos_sin_strides, 2) &&
+                   vec_tensor(sin, cos_sin_strides, 2);
+  const dim3 grid(static_cast<unsigned>(n_rows));
+  hipStream_t st = as_stream(stream);
+#define LAUNCH(T)                                                                                        \
+  do {                                                                                                   \
+    if (vec) hipLaunchKernelGGL((rope_kv_append_kernel<T, true>), grid, dim3(kThreads), 0, st, a);       \
+    else hipLaunchKernelGGL((rope_kv_append_kernel<T, false>), grid, dim3(kThreads), 0, st, a);          \
+  } while (0)
+  switch (dtype) {
+    case RLT_BFLOAT16: LAUNCH(bf16); break;
+    case RLT_FLOAT16: LAUNCH(f16); break;
+    default: LAUNCH(float); break;
+  }
+#undef LAUNCH
+  return check_launch("rlt_rope_kv_append");
 }
 
 extern "C" int rlt_kv_copy_token(void* key_cache, void* value_cache, const int64_t* cache_strides, int64_t src_block,

@@ -39,6 +39,13 @@ SIGNATURES = {
         + [c_int64] * 7
         + [c_int, c_void_p],
     ),
+    "rlt_rope_kv_append": (
+        c_int,
+        [c_void_p, c_void_p, _i64p, c_void_p, _i64p, c_void_p, _i64p, c_void_p, _i64p, c_void_p, c_void_p, _i64p]
+        + [c_void_p, _i64p, c_void_p, c_void_p]
+        + [c_int64] * 9
+        + [c_int, c_void_p],
+    ),
     "rlt_paged_decode_workspace_bytes": (c_int64, [c_int64] * 4),
     "rlt_paged_decode": (
         c_int,

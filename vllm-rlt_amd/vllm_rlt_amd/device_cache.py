@@ -19,6 +19,13 @@ class DeviceCache:
         cache = self.cache
         ops.kv_append(cache.key_cache, cache.value_cache, layer, batch.write_blocks, batch.write_offsets, k, v)
 
+    def _write_prepared_rotary(self, layer, batch, q, k, v, position_embeddings):
+        cache = self.cache
+        cos, sin = position_embeddings
+        return ops.rope_kv_append(
+            cache.key_cache, cache.value_cache, layer, batch.write_blocks, batch.write_offsets, q, k, v, cos, sin
+        )
+
     def _attend_prepared(self, layer, batch, q):
         cache = self.cache
         return cache.attention(

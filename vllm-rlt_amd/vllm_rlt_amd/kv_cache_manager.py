@@ -169,6 +169,39 @@ class KVCacheManager(KVPageBook):
         self._record_written(batch, layer)
 
     @torch.no_grad()
+    def _write_prepared_rotary(
+        self,
+        layer: int,
+        batch: PreparedKVBatch,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        position_embeddings: tuple[torch.Tensor, torch.Tensor],
+    ) -> torch.Tensor:
+        """Rotate q and k and append the rows' K/V in one launch; returns rotated q.
+
+        The fused form of the caller's rotation (vllm_rlt/models/ouro.py:104-109,
+        q * cos + rotate_half(q) * sin with the traversal's position_embeddings)
+        followed by _write_prepared (:520-534).  Pages and the returned q are
+        bit-identical to the unfused sequence.
+        """
+        self._validate_layer(layer)
+        self._require_live_batch(batch)
+        if not batch.writable:
+            raise ValueError("a read-only prepared KV batch cannot be written")
+        self._validate_tensor(q, len(batch.position_ids), "q", query=True)
+        self._validate_tensor(k, len(batch.position_ids), "k")
+        self._validate_tensor(v, len(batch.position_ids), "v")
+        cos, sin = position_embeddings
+        out = ops.rope_kv_append(
+            self.key_cache, self.value_cache, layer, batch.write_blocks, batch.write_offsets, q, k, v, cos, sin,
+            n_rows=len(batch.rows),
+        )
+        if batch.rows:
+            self._record_written(batch, layer)
+        return out
+
+    @torch.no_grad()
     def attend(self, layer, request_ids, depths, positions, q) -> torch.Tensor:
         """Causal GQA at each row's own position and recurrence depth (:545-557)."""
         self._validate_layer(layer)

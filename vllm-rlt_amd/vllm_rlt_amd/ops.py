@@ -87,6 +87,95 @@ def kv_append(
     check(rc, "rlt_kv_append")
 
 
+def rope_kv_append(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    layer: int,
+    write_blocks: torch.Tensor,
+    write_offsets: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    out: torch.Tensor | None = None,
+    n_rows: int | None = None,
+) -> torch.Tensor:
+    """Rotate q and k by (cos, sin), append rotated k and v; returns rotated q.
+
+    One launch for the rotation of vllm_rlt/models/ouro.py:104-109
+    (q * cos + rotate_half(q) * sin, same for k) and the index_put pair of
+    vllm_rlt/core/kv_cache_manager.py:531-532.  cos and sin are the per-row
+    [batch, head_dim] tables the model computes once per traversal (a
+    broadcast [batch, 1, head_dim] view is accepted).  Rows below n_rows
+    (default: all of write_blocks) are written; q is rotated for every row.
+    `out` may be q itself.
+    """
+    device = _require_rocm(key_cache, value_cache, write_blocks, write_offsets, q, k, v, cos, sin)
+    if key_cache.shape != value_cache.shape or key_cache.stride() != value_cache.stride():
+        raise ValueError("key_cache and value_cache must share shape and strides")
+    if key_cache.ndim != 5:
+        raise ValueError("caches must be [blocks, layers, page, kv_heads, head_dim]")
+    nb, nl, page, hkv, d = key_cache.shape
+    if d % 2:
+        raise ValueError("head_dim must be even for split-half RoPE")
+    rows = q.shape[0]
+    if q.ndim != 3 or q.shape[2] != d or q.shape[1] % hkv:
+        raise ValueError(f"q must have shape [batch, heads, {d}] with heads a multiple of {hkv}")
+    for t, name in ((k, "k"), (v, "v")):
+        if t.ndim != 3 or t.shape != (rows, hkv, d):
+            raise ValueError(f"{name} must have shape [{rows}, {hkv}, {d}]")
+    if cos.ndim == 3 and cos.shape[1] == 1:
+        cos = cos[:, 0]
+    if sin.ndim == 3 and sin.shape[1] == 1:
+        sin = sin[:, 0]
+    if cos.shape != (rows, d) or sin.shape != (rows, d) or cos.stride() != sin.stride():
+        raise ValueError(f"cos and sin must be [{rows}, {d}] with equal strides")
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (cos, "cos"), (sin, "sin")):
+        if t.dtype != key_cache.dtype:
+            raise ValueError(f"{name} must use dtype {key_cache.dtype}")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError("out must match q")
+    _require_int(write_blocks, torch.int64, "write_blocks")
+    _require_int(write_offsets, torch.int64, "write_offsets")
+    n = len(write_blocks) if n_rows is None else n_rows
+    if n > min(len(write_blocks), len(write_offsets), rows):
+        raise ValueError("n_rows exceeds the provided rows")
+    rc = _native.load().rlt_rope_kv_append(
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int64_array(key_cache.stride()),
+        q.data_ptr(),
+        int64_array(q.stride()),
+        k.data_ptr(),
+        int64_array(k.stride()),
+        v.data_ptr(),
+        int64_array(v.stride()),
+        cos.data_ptr(),
+        sin.data_ptr(),
+        int64_array(cos.stride()),
+        out.data_ptr(),
+        int64_array(out.stride()),
+        write_blocks.data_ptr(),
+        write_offsets.data_ptr(),
+        rows,
+        n,
+        layer,
+        nl,
+        nb,
+        page,
+        q.shape[1],
+        hkv,
+        d,
+        dtype_code(key_cache.dtype),
+        stream_handle(device),
+    )
+    check(rc, "rlt_rope_kv_append")
+    return out
+
+
 def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
     return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))
 
