@@ -98,6 +98,29 @@ int rlt_rope_kv_append(void* key_cache, void* value_cache, const int64_t* cache_
                        int64_t num_kv_heads, int64_t head_dim, int dtype, void* stream);
 
 /*
+ * Gather of slot-indexed per-request rows into batch order.
+ * Replaces gather_kernel (vllm_rlt/kernels/routing.py:45-59), launched by
+ * RoutingBank.gather (vllm_rlt/worker/async_state.py:93-102):
+ *   out[r] = pool[slots[r]]  for r < count;  out[r] = 0 for count <= r < size
+ * Rows are row_bytes long (hidden states, int64 tokens, any dtype); strides are
+ * in bytes.  A slot outside [0, num_slots) reads as zeros.
+ */
+int rlt_gather_rows(const void* pool, int64_t pool_row_bytes_stride, int64_t num_slots,
+                    const int64_t* slots, int64_t count, int64_t size, void* out,
+                    int64_t out_row_bytes_stride, int64_t row_bytes, void* stream);
+
+/*
+ * Scatter of batch rows back to their request slots.
+ * Replaces scatter_kernel (vllm_rlt/kernels/routing.py:62-76), launched by
+ * RoutingBank.scatter (vllm_rlt/worker/async_state.py:104-112):
+ *   pool[slots[r]] = values[r]  for r < count
+ * Strides in bytes; a slot outside [0, num_slots) is skipped.
+ */
+int rlt_scatter_rows(const void* values, int64_t values_row_bytes_stride, const int64_t* slots,
+                     int64_t count, void* pool, int64_t pool_row_bytes_stride, int64_t num_slots,
+                     int64_t row_bytes, void* stream);
+
+/*
  * Workspace bytes rlt_paged_decode needs for n_rows rows.  Depends only on the
  * shape, never on context lengths, so a caller can size it without a sync.
  */

@@ -6,17 +6,22 @@ include/rlt_kv.h).
 """
 
 from . import ops
+from .async_state import AsyncState, RoutingBank
 from .device_cache import DeviceCache
+from .graphs import RecurrentGraphs
 from .kv_cache_manager import KVCacheManager
 from .page_book import KVPageBook, PreparedKVBatch
 from .paged_attention import HipPagedAttention, hip_paged_attention
 
 __all__ = [
+    "AsyncState",
     "DeviceCache",
     "HipPagedAttention",
     "KVCacheManager",
     "KVPageBook",
     "PreparedKVBatch",
+    "RecurrentGraphs",
+    "RoutingBank",
     "hip_paged_attention",
     "ops",
 ]

@@ -46,6 +46,14 @@ SIGNATURES = {
         + [c_int64] * 9
         + [c_int, c_void_p],
     ),
+    "rlt_gather_rows": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p],
+    ),
+    "rlt_scatter_rows": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p],
+    ),
     "rlt_paged_decode_workspace_bytes": (c_int64, [c_int64] * 4),
     "rlt_paged_decode": (
         c_int,

@@ -176,6 +176,50 @@ def rope_kv_append(
     return out
 
 
+def _row_bytes(t: torch.Tensor, name: str) -> int:
+    if t.ndim != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D with contiguous rows")
+    return t.shape[1] * t.element_size()
+
+
+def gather_rows(pool: torch.Tensor, slots: torch.Tensor, out: torch.Tensor, count: int) -> torch.Tensor:
+    """out[r] = pool[slots[r]] for r < count, zeros for the remaining rows of out.
+
+    gather_kernel of vllm_rlt/kernels/routing.py:45-59 (RoutingBank.gather,
+    vllm_rlt/worker/async_state.py:93-102).  Returns out.
+    """
+    device = _require_rocm(pool, slots, out)
+    _require_int(slots, torch.int64, "slots")
+    row_bytes = _row_bytes(pool, "pool")
+    if _row_bytes(out, "out") != row_bytes or out.dtype != pool.dtype:
+        raise ValueError("out rows must match pool rows")
+    if not 0 <= count <= min(out.shape[0], slots.numel()):
+        raise ValueError("count exceeds the rows of out or slots")
+    rc = _native.load().rlt_gather_rows(
+        pool.data_ptr(), pool.stride(0) * pool.element_size(), pool.shape[0], slots.data_ptr(), count,
+        out.shape[0], out.data_ptr(), out.stride(0) * out.element_size(), row_bytes, stream_handle(device),
+    )
+    check(rc, "rlt_gather_rows")
+    return out
+
+
+def scatter_rows(values: torch.Tensor, slots: torch.Tensor, pool: torch.Tensor, count: int | None = None) -> None:
+    """pool[slots[r]] = values[r] for r < count (scatter_kernel, vllm_rlt/kernels/routing.py:62-76)."""
+    device = _require_rocm(values, slots, pool)
+    _require_int(slots, torch.int64, "slots")
+    row_bytes = _row_bytes(pool, "pool")
+    if _row_bytes(values, "values") != row_bytes or values.dtype != pool.dtype:
+        raise ValueError("values rows must match pool rows")
+    n = values.shape[0] if count is None else count
+    if not 0 <= n <= min(values.shape[0], slots.numel()):
+        raise ValueError("count exceeds the rows of values or slots")
+    rc = _native.load().rlt_scatter_rows(
+        values.data_ptr(), values.stride(0) * values.element_size(), slots.data_ptr(), n, pool.data_ptr(),
+        pool.stride(0) * pool.element_size(), pool.shape[0], row_bytes, stream_handle(device),
+    )
+    check(rc, "rlt_scatter_rows")
+
+
 def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
     return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))
 
