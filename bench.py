@@ -54,6 +54,9 @@ WORKLOADS = {
     "ouro-prefix-stress": dict(
         batch=64, ctx=(16384, 32768), planes=1, depth_probs=None, refill=False, prefix=8192
     ),
+    # The reference CPU case's shape (batch 4, contexts U[1, 256]) over all 24
+    # layers and 4 planes: launch-bound, where graph replay matters.
+    "ouro-small-batch": dict(batch=4, ctx=(1, 256), planes=LOOPS, depth_probs=None, refill=False, prefix=0),
 }
 # SHARED refill: a request finishes after U{1..8} generated tokens.
 REFILL_TOKENS = (1, 8)
@@ -72,6 +75,11 @@ def parse_args():
     p.add_argument("--cpu-reps", type=int, default=3, help="timed repetitions of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-check", action="store_true", help="skip the pre-timing parity spot check")
+    p.add_argument(
+        "--graph",
+        action="store_true",
+        help="decode workloads: capture one loop-step in a HIP graph and time its replays",
+    )
     p.add_argument(
         "--calibrate-counters",
         action="store_true",
@@ -292,12 +300,12 @@ class Workload:
         return torch.equal(self.key_cache[idx], snapshot[0]) and torch.equal(self.value_cache[idx], snapshot[1])
 
 
-def build_metadata(w, step):
+def build_metadata(w, step, descriptors=None):
     from vllm_rlt_amd import ops
 
     ops.build_decode_metadata(
-        w.descriptors[step], w.batch, w.batch, w.tables, PAGE, w.slots, w.positions, w.lengths,
-        w.blocks, w.offsets, w.row_tables, w.width,
+        w.descriptors[step] if descriptors is None else descriptors, w.batch, w.batch, w.tables, PAGE, w.slots,
+        w.positions, w.lengths, w.blocks, w.offsets, w.row_tables, w.width,
     )
 
 
@@ -311,10 +319,28 @@ def layer_step(w, layer):
     )
 
 
-def loop_step(w, step):
-    build_metadata(w, step)
+def loop_step(w, step, descriptors=None):
+    build_metadata(w, step, descriptors)
     for layer in range(LAYERS):
         layer_step(w, layer)
+
+
+def capture_loop_step(w):
+    """One loop-step captured in a HIP graph; its descriptors are read from a static buffer."""
+    static = torch.empty_like(w.descriptors[0])
+    static.copy_(w.descriptors[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            loop_step(w, 0, static)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loop_step(w, 0, static)
+    torch.cuda.synchronize()
+    return graph, static
 
 
 def step_bytes(lengths, shared_tokens=0):
@@ -621,12 +647,30 @@ def main():
         total_bytes += b
         decode_bytes.append(d)
         unique_bytes.append(u)
+    graph = None
+    if args.graph:
+        graph, static = capture_loop_step(w)
+        for step in range(args.warmup):  # warm the replay path too
+            static.copy_(w.descriptors[step])
+            graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for step in range(args.warmup, total):
-        loop_step(w, step)
+    if graph is None:
+        for step in range(args.warmup, total):
+            loop_step(w, step)
+    else:
+        for step in range(args.warmup, total):
+            static.copy_(w.descriptors[step])
+            graph.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    if graph is not None:
+        # The replayed steps must leave the same outputs as eager steps.
+        last = w.out.clone()
+        loop_step(w, total - 1)
+        torch.cuda.synchronize()
+        if not torch.equal(last.view(torch.int16), w.out.view(torch.int16)):
+            raise SystemExit("graph replay differs from eager execution")
 
     # Decode-launch timing with HIP events on the launch stream (separate pass,
     # same steps): each event pair brackets one rlt_paged_decode call.
@@ -679,6 +723,7 @@ def main():
             "global_batch": w.batch,
             "seq_len": int(w.contexts.float().mean().item()),
             "parallelism": "single-gpu",
+            "launch": "hip-graph replay" if graph is not None else "eager",
         },
         "hbm_gb_per_s": round(gbs, 1),
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
