@@ -121,6 +121,38 @@ int rlt_scatter_rows(const void* values, int64_t values_row_bytes_stride, const 
                      int64_t row_bytes, void* stream);
 
 /*
+ * Whole-page export / import of the K and V pools (all layers of a page are one
+ * contiguous block).  Replaces the page-by-page copies of preemption
+ *   keys[row] = key_cache[block]   (vllm_rlt/engine/preemption.py:85-89)
+ *   key_cache[block] = keys[row]   (vllm_rlt/engine/preemption.py:130-132)
+ * and the whole-page segments of kv_segments (vllm_rlt/pd/transport.py:35-37):
+ *   export: dst_keys[i] = key_cache[blocks[i]], dst_values[i] = value_cache[blocks[i]]
+ *   import: key_cache[blocks[i]] = src_keys[i], value_cache[blocks[i]] = src_values[i]
+ * for i < n, page_bytes per page.  Strides in bytes.  The packed rows may be
+ * device memory or pinned host memory.  A block id outside [0, num_blocks) is
+ * skipped.
+ */
+int rlt_kv_export_pages(const void* key_cache, const void* value_cache, int64_t pool_stride_bytes,
+                        int64_t page_bytes, int64_t num_blocks, const int64_t* blocks, int64_t n,
+                        void* dst_keys, void* dst_values, int64_t dst_stride_bytes, void* stream);
+int rlt_kv_import_pages(void* key_cache, void* value_cache, int64_t pool_stride_bytes,
+                        int64_t page_bytes, int64_t num_blocks, const int64_t* blocks, int64_t n,
+                        const void* src_keys, const void* src_values, int64_t src_stride_bytes,
+                        void* stream);
+
+/*
+ * Batched byte-range copy: dst_addresses[i][0:bytes[i]] = src_addresses[i][0:bytes[i]]
+ * for i < n, one launch.  Executes the (address, size) descriptor lists of
+ * kv_segments / partition_segments (vllm_rlt/pd/transport.py:18-68) for a
+ * transfer the device can address directly (same device, or peer / pinned
+ * host memory mapped to it).  The three arrays are device or pinned host
+ * memory; max_bytes (the largest bytes[i]) only sizes the grid.  The caller
+ * guarantees every range lies inside its allocation.
+ */
+int rlt_copy_segments(const int64_t* src_addresses, const int64_t* dst_addresses,
+                      const int64_t* bytes, int64_t n, int64_t max_bytes, void* stream);
+
+/*
  * Workspace bytes rlt_paged_decode needs for n_rows rows.  Depends only on the
  * shape, never on context lengths, so a caller can size it without a sync.
  */

@@ -54,6 +54,15 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p],
     ),
+    "rlt_kv_export_pages": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
+    "rlt_kv_import_pages": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
+    "rlt_copy_segments": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "rlt_paged_decode_workspace_bytes": (c_int64, [c_int64] * 4),
     "rlt_paged_decode": (
         c_int,
