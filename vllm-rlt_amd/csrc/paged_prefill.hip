@@ -75,6 +75,38 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(1))) void global_void;
+
+// Direct global->LDS loads.  They are written as assembly so that the
+// compiler's wait analysis, which cannot tell the tile buffers apart, does not
+// wait for a tile still in flight before reading the previous one: the
+// kernel orders them itself with explicit vmcnt waits and barriers.  Lane l
+// writes bytes [l*16, l*16 + 16) (dword form: [l*4, l*4 + 4)) after the LDS
+// byte address in M0.  The kernel uses M0 for nothing else.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(uint32_t lds_byte, uint32_t offset, uint64_t base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_byte), "v"(offset), "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(uint32_t lds_byte, const void* address) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_byte), "v"(address)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <typename P>
+__device__ __forceinline__ uint32_t lds_address(P* p) {
+  return static_cast<uint32_t>(uniform(static_cast<int>((uint32_t)(uintptr_t)(lds_u16*)(p))));
+}
+
+// Position of logical 16-byte chunk c of LDS row r is c ^ lds_swizzle(r & 15):
+// a bijection on 0..15, so 16 consecutive rows put one logical chunk in 16
+// distinct bank groups, and 4 consecutive rows (from a multiple of 4) put a
+// chunk pair in 8.
+__device__ __forceinline__ int lds_swizzle(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
@@ -161,19 +193,25 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
 // item = (seq * max_qt + t) * hq + head; empty items exit.
 constexpr int kXcds = 8;
 constexpr int kRankSeqs = 512;  // ranked mode: at most this many sequences
+constexpr int kTablePages = 4096;  // page ids staged in LDS per workgroup (65536 keys)
 
-template <typename T, int D>
+template <typename T, int D, bool DMA>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_mfma_kernel(PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   constexpr int KSTEPS = D / 16;  // q.k k-steps
   constexpr int DTILES = D / 32;  // output column tiles
-  // Row strides in elements.  K: a quarter-wave's 16-byte reads of 16 rows
-  // land in distinct bank groups when the stride is an odd multiple of 16
-  // bytes.  V: the transposing read takes 4 rows x 64 bytes per half-wave, so
-  // the stride is 64 (mod 256) bytes.
-  constexpr int KROW = D + 8;
-  constexpr int VROW = D + 32;
+  // DMA (head_dim 128, page table within kTablePages): K/V tiles go from global memory straight into LDS
+  // (global_load_lds_dwordx4), unpadded 256-byte rows whose 16-byte chunks are
+  // XOR-swizzled (chunk c of row r sits at position c ^ lds_swizzle(r)) so the
+  // K reads and the transposing V reads stay free of bank conflicts.  Other
+  // head sizes stage through registers into padded rows: K, a quarter-wave's
+  // 16-byte reads of 16 rows land in distinct bank groups when the stride is
+  // an odd multiple of 16 bytes; V, the transposing read takes 4 rows x 64
+  // bytes per half-wave, so the stride is 64 (mod 256) bytes.
+  static_assert(!DMA || D == 128, "direct-to-LDS staging is laid out for head_dim 128");
+  constexpr int KROW = DMA ? D : D + 8;
+  constexpr int VROW = DMA ? D : D + 32;
   constexpr int KT = kBN * KROW, VT = kBN * VROW;  // elements per K / V tile
   constexpr int CHUNKS = D / 8;  // 16-byte chunks per token row
   constexpr int TOKENS_PER_PASS = 256 / CHUNKS;
@@ -188,6 +226,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // Two key groups, each with two K and V tile buffers; reused for ranking
   // before the tile loop and for the key-group merge after it.
   __shared__ __align__(16) uint16_t lds[4 * (KT + VT)];
+  // Landing area of the L2 prefetches (never read): one dword per lane.
+  __shared__ __align__(16) uint32_t prefetch_sink[DMA ? 8 * 64 : 1];
+  // Page ids of the workgroup's key range (direct-to-LDS path), staged once so
+  // that the tile loop reads them from LDS rather than global memory.
+  __shared__ int32_t page_ids[DMA ? kTablePages : 1];
 
   const int tid = threadIdx.x;
   int seq, t, h;
@@ -309,6 +352,60 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   auto table_chunk = [&](int c) { return trow[min(c * 64 + lane, last_page)]; };
   int32_t tab_cur = table_chunk(0), tab_next = table_chunk(1);
   u32x4 kreg[PASSES], vreg[PASSES];
+  // Direct-to-LDS staging: wave qw of a key group fills page 4j + qw of tile
+  // j, rows 16qw .. 16qw+15 of the K and V tiles, four rows per instruction.
+  // Lane l writes row 16qw + 4i + l/16 at chunk position l%16, so it fetches
+  // that token's logical chunk (l%16) ^ lds_swizzle(4i + l/16).
+  uint32_t dma_full[4], dma_last[4];
+  if constexpr (DMA) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int slot = 4 * i + (lane >> 4);
+      const int chunk = (lane & 15) ^ lds_swizzle(slot);
+      dma_full[i] = static_cast<uint32_t>((slot * a.kv_token + chunk * 8) * sizeof(T));
+      dma_last[i] = static_cast<uint32_t>((min(slot, last_slot) * a.kv_token + chunk * 8) * sizeof(T));
+    }
+  }
+  // L2 prefetch of the page a wave will stage two tiles later: lanes 0-31
+  // touch the 32 cache lines of its K head slices, lanes 32-63 those of V.
+  // Every address stays inside the page's block.
+  const char* pf_k = kbase;
+  const char* pf_v = vbase;
+  const uint32_t pf_off = static_cast<uint32_t>(((lane & 31) >> 1) * a.kv_token * sizeof(T) + (lane & 1) * 128);
+  // Page p of the sequence (p < 4 * ntiles, which the host keeps within
+  // kTablePages); past the last valid page the last page's id.
+  auto page_id = [&](int p) -> uint32_t { return static_cast<uint32_t>(uniform(page_ids[min(p, kTablePages - 1)])); };
+  auto prefetch_tile = [&](int j) {
+    const int p = j * (kBN / kPage) + qw;
+    if (j < ntiles) {
+      const uint32_t id = page_id(p);
+      const int64_t blk = id < nblocks ? id : 0;
+      pf_k = kbase + blk * block_bytes;
+      pf_v = vbase + blk * block_bytes;
+    }
+    const char* src = (lane < 32 ? pf_k : pf_v) + pf_off;
+    lds_dma4(lds_address(prefetch_sink + wave * 64), src);
+  };
+  auto issue_tile = [&](int j, int b) {
+    const int p = j * (kBN / kPage) + qw;
+    const uint32_t id = page_id(p);
+    const int64_t blk = id < nblocks ? id : 0;
+    const char* kp = kbase + blk * block_bytes;
+    const char* vp = vbase + blk * block_bytes;
+    pf_k = kp;
+    pf_v = vp;
+    // LDS byte address of this wave's rows in buffer b (uniform).
+    const uint32_t kd = lds_address(group_lds + b * (KT + VT) + qw * 16 * KROW);
+    const uint32_t vd = kd + KT * sizeof(uint16_t);
+    const uint64_t ks = uniform64(reinterpret_cast<int64_t>(kp));
+    const uint64_t vs = uniform64(reinterpret_cast<int64_t>(vp));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t off = p >= last_page ? dma_last[i] : dma_full[i];
+      lds_dma16(kd + i * 4 * KROW * sizeof(uint16_t), off, ks);
+      lds_dma16(vd + i * 4 * KROW * sizeof(uint16_t), off, vs);
+    }
+  };
   // Tiles of a key group arrive 2 apart: the group's first tile of chunk c
   // is 16c + kg.
   auto load_tile = [&](int j) {
@@ -332,6 +429,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // the key order of the P^T B operand below.
   const int grp = lane >> 4, gl = lane & 15;
   const int tr_off = (4 * (grp >> 1) + (gl >> 2)) * VROW + 16 * (grp & 1) + 4 * (gl & 3);
+  // Swizzled layout: a lane's K row is col (+32), its logical chunk 2ks + half;
+  // its V rows are rlo and rlo + 8, logical chunk 4c + 2(grp&1) + (gl&3)/2,
+  // 8-byte half gl&1 (rows 16ks + r keep r's swizzle).
+  const int kswz = lds_swizzle(col & 15);
+  int v_lo[DTILES], v_hi[DTILES];
+  if constexpr (DMA) {
+    const int rlo = 4 * (grp >> 1) + (gl >> 2);
+    const int m0 = 2 * (grp & 1) + ((gl & 3) >> 1);
+#pragma unroll
+    for (int c = 0; c < DTILES; ++c) {
+      v_lo[c] = rlo * KROW + (((4 * c + m0) ^ lds_swizzle(rlo)) * 8) + 4 * (gl & 1);
+      v_hi[c] = (rlo + 8) * KROW + (((4 * c + m0) ^ lds_swizzle(rlo + 8)) * 8) + 4 * (gl & 1);
+    }
+  }
 
   f32x16 acc_o[DTILES];
 #pragma unroll
@@ -352,15 +463,44 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       *reinterpret_cast<u32x4*>(&vb[tok * VROW + ld_chunk * 8]) = vreg[i];
     }
   };
-  if (kg < ntiles) {
-    load_tile(kg);
-    store_tile(0);
+  // Exactly one vector-memory load, the prefetch, follows a tile's staging
+  // loads, so waiting for all but the newest load (vmcnt(1)) completes the
+  // tile's loads while the prefetch stays in flight.  sched_barrier keeps
+  // the prefetch after the staging loads.
+  auto tile_barrier = [&]() { asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  if constexpr (DMA) {
+    const int fill = min(4 * ntiles, kTablePages);
+    for (int i = tid; i < fill; i += 512) page_ids[i] = trow[min(i, last_page)];
+    __syncthreads();
+    // The tile of iteration it arrives during iteration it - 1; the barrier
+    // at the top of each iteration (after this wave's staging loads landed)
+    // makes every wave's share visible, and the next tile's loads then go to
+    // the buffer every wave finished reading before that barrier.  The page
+    // two tiles further on is prefetched into L2 meanwhile.
+    if (kg < ntiles) {
+      issue_tile(kg, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      prefetch_tile(kg + 2);
+    }
+  } else {
+    if (kg < ntiles) {
+      load_tile(kg);
+      store_tile(0);
+    }
+    if (kg + 2 < ntiles) load_tile(kg + 2);
+    __syncthreads();
   }
-  if (kg + 2 < ntiles) load_tile(kg + 2);
-  __syncthreads();
   const int niter = (ntiles + 1) / 2;
   for (int it = 0; it < niter; ++it) {
     const int j = 2 * it + kg;
+    if constexpr (DMA) {
+      tile_barrier();
+      if (kg < ntiles) {
+        if (j + 2 < ntiles) issue_tile(j + 2, (it + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        prefetch_tile(j + 4);
+      }
+    }
     const uint16_t* k_lds = group_lds + (it & 1) * (KT + VT);
     const uint16_t* v_lds = k_lds + KT;
     const int key0 = j * kBN;
@@ -372,7 +512,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       f32x16 c = {};
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
-        const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
+        const int kcol = DMA ? (((2 * ks + half) ^ kswz) * 8) : ks * 16 + half * 8;
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + kcol]);
         c = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c);
       }
       sacc[hh] = c;
@@ -431,22 +572,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int e = 0; e < 4; ++e) pb[e] = Ops::pack2(sacc[hh][base + 2 * e], sacc[hh][base + 2 * e + 1]);
 #pragma unroll
       for (int c = 0; c < DTILES; ++c) {
-        const uint16_t* vp = &v_lds[tr_off + ks * 16 * VROW + c * 32];
-        const u32x2 lo = lds_read_tr(vp);
-        const u32x2 hi = lds_read_tr(vp + 8 * VROW);
+        const uint16_t* vlo = DMA ? &v_lds[v_lo[c] + ks * 16 * VROW] : &v_lds[tr_off + ks * 16 * VROW + c * 32];
+        const uint16_t* vhi = DMA ? &v_lds[v_hi[c] + ks * 16 * VROW] : vlo + 8 * VROW;
+        const u32x2 lo = lds_read_tr(vlo);
+        const u32x2 hi = lds_read_tr(vhi);
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
         acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
       }
     }
     }
-    if (j + 2 < ntiles) store_tile((it + 1) & 1);
-    __syncthreads();
-    if (j + 4 < ntiles) load_tile(j + 4);
+    if constexpr (!DMA) {
+      if (j + 2 < ntiles) store_tile((it + 1) & 1);
+      __syncthreads();
+      if (j + 4 < ntiles) load_tile(j + 4);
+    }
   }
+  if constexpr (DMA) __syncthreads();  // every tile read before the merge reuses LDS
 
   // Merge the key groups: group 1 hands (m, l, acc) to group 0 through LDS,
-  // laid out [query wave][value][lane] (the loop's last barrier ordered every
-  // tile read before these writes).
+  // laid out [query wave][value][lane] (the last barrier ordered every tile
+  // read before these writes).
   float* xs = reinterpret_cast<float*>(lds) + qw * MERGE_FLOATS * 64 + lane;
   if (kg == 1) {
     xs[0] = m;
@@ -589,12 +734,16 @@ extern "C" int rlt_paged_prefill(const void* q, const int64_t* q_strides, const 
     if (items == 0) return RLT_OK;
     const dim3 grid(static_cast<unsigned>(items));
     hipStream_t st = as_stream(stream);
+    // Direct-to-LDS staging needs the key range's page ids to fit in LDS.
+    const bool dma = head_dim == 128 && max_table_width <= kTablePages;
     if (dtype == RLT_BFLOAT16) {
-      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 128>), grid, dim3(512), 0, st, p);
-      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 64>), grid, dim3(512), 0, st, p);
+      if (dma) hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 128, true>), grid, dim3(512), 0, st, p);
+      else if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 128, false>), grid, dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<bf16, 64, false>), grid, dim3(512), 0, st, p);
     } else {
-      if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 128>), grid, dim3(512), 0, st, p);
-      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 64>), grid, dim3(512), 0, st, p);
+      if (dma) hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 128, true>), grid, dim3(512), 0, st, p);
+      else if (head_dim == 128) hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 128, false>), grid, dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((paged_prefill_mfma_kernel<f16, 64, false>), grid, dim3(512), 0, st, p);
     }
     return check_launch("rlt_paged_prefill");
   }
