@@ -102,11 +102,34 @@ __device__ __forceinline__ uint32_t lds_address(P* p) {
   return static_cast<uint32_t>(uniform(static_cast<int>((uint32_t)(uintptr_t)(lds_u16*)(p))));
 }
 
-// Position of logical 16-byte chunk c of LDS row r is c ^ lds_swizzle(r & 15):
-// a bijection on 0..15, so 16 consecutive rows put one logical chunk in 16
-// distinct bank groups, and 4 consecutive rows (from a multiple of 4) put a
-// chunk pair in 8.
-__device__ __forceinline__ int lds_swizzle(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// Position of logical 16-byte chunk c of LDS row r (256 bytes) is
+// c ^ lds_swizzle(r).  The 32 banks span 128 bytes, i.e. 8 chunk positions,
+// and a 16-byte read serves 8 consecutive lanes per pass: since the swizzle's
+// low 3 bits are a bijection of r % 8, 8 consecutive rows put one logical
+// chunk in 8 distinct bank groups (the K reads).  An 8-byte read serves 16
+// lanes per pass; bits 1-2 are a bijection of r % 4, so 4 consecutive rows
+// from a multiple of 4 put an aligned chunk pair in 4 distinct 32-byte
+// groups (the transposing V reads).  Rows r and r + 8 share a swizzle.
+__device__ __forceinline__ int lds_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// x, as a value the compiler cannot see through: addresses derived from it
+// are recomputed where they are used (a few integer operations) instead of
+// being hoisted out of the tile loop, where they would hold registers.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges one
+// register's upper 32 lanes with another's lower 32, so two copies of x end
+// up holding the two halves' values in swapped order, whichever way round.
+// The waits cover the VALU->permlane and permlane->VALU hazards, which the
+// compiler does not see inside assembly.
+__device__ __forceinline__ float max_across_halves(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
 
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
@@ -307,7 +330,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // Waves 0-3 take key tiles 0, 2, 4, ...; waves 4-7 tiles 1, 3, 5, ...; wave
   // w and w + 4 own the same 32 query rows and merge at the end.
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);  // scalar, so per-wave conditions branch on SCC
   const int kg = wave >> 2;   // key group
   const int qw = wave & 3;    // query wave within the group
   const int gtid = tid & 255; // thread within the key group
@@ -356,55 +379,58 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // j, rows 16qw .. 16qw+15 of the K and V tiles, four rows per instruction.
   // Lane l writes row 16qw + 4i + l/16 at chunk position l%16, so it fetches
   // that token's logical chunk (l%16) ^ lds_swizzle(4i + l/16).
+  auto dma_offset = [&](int ln, int i, int slot_limit) {
+    const int slot = 4 * i + (ln >> 4);
+    const int chunk = (ln & 15) ^ lds_swizzle(slot);
+    return static_cast<uint32_t>((min(slot, slot_limit) * a.kv_token + chunk * 8) * sizeof(T));
+  };
+  // Page p of the sequence (p < 4 * ntiles, which the host keeps within
+  // kTablePages); past the last valid page the last page's id.  page_slot
+  // reads the entry into a vector register (its use can come a phase later),
+  // page_id makes it scalar.
+  auto page_slot = [&](int p) -> int32_t { return page_ids[min(p, kTablePages - 1)]; };
+  auto page_id = [&](int p) -> uint32_t { return static_cast<uint32_t>(uniform(page_slot(p))); };
+  // Page p of tile j that wave qw stages; tiles past the last are clamped.
+  auto tile_page = [&](int j) { return min(j, ntiles - 1) * (kBN / kPage) + qw; };
+  // Per-lane source offsets of the four staging instructions of a page, and
+  // of the sequence's last page (whose slots past the last key re-read it).
   uint32_t dma_full[4], dma_last[4];
   if constexpr (DMA) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int slot = 4 * i + (lane >> 4);
-      const int chunk = (lane & 15) ^ lds_swizzle(slot);
-      dma_full[i] = static_cast<uint32_t>((slot * a.kv_token + chunk * 8) * sizeof(T));
-      dma_last[i] = static_cast<uint32_t>((min(slot, last_slot) * a.kv_token + chunk * 8) * sizeof(T));
+      dma_full[i] = dma_offset(lane, i, kPage - 1);
+      dma_last[i] = dma_offset(lane, i, last_slot);
     }
   }
-  // L2 prefetch of the page a wave will stage two tiles later: lanes 0-31
-  // touch the 32 cache lines of its K head slices, lanes 32-63 those of V.
-  // Every address stays inside the page's block.
-  const char* pf_k = kbase;
-  const char* pf_v = vbase;
-  const uint32_t pf_off = static_cast<uint32_t>(((lane & 31) >> 1) * a.kv_token * sizeof(T) + (lane & 1) * 128);
-  // Page p of the sequence (p < 4 * ntiles, which the host keeps within
-  // kTablePages); past the last valid page the last page's id.
-  auto page_id = [&](int p) -> uint32_t { return static_cast<uint32_t>(uniform(page_ids[min(p, kTablePages - 1)])); };
-  auto prefetch_tile = [&](int j) {
-    const int p = j * (kBN / kPage) + qw;
-    if (j < ntiles) {
-      const uint32_t id = page_id(p);
-      const int64_t blk = id < nblocks ? id : 0;
-      pf_k = kbase + blk * block_bytes;
-      pf_v = vbase + blk * block_bytes;
-    }
-    const char* src = (lane < 32 ? pf_k : pf_v) + pf_off;
-    lds_dma4(lds_address(prefetch_sink + wave * 64), src);
+  // One staging half: the K (which 0) or V (which 1) rows of page p (id
+  // `id`) bound for buffer b of the wave's key group, where wave qw fills
+  // rows 16qw .. 16qw + 15; issue(i) sends rows 16qw + 4i .. + 3.
+  struct StageHalf {
+    uint32_t dst;   // LDS byte address of the wave's rows
+    uint64_t src;   // page base in global memory
+    bool last;      // page p is the sequence's last
   };
-  auto issue_tile = [&](int j, int b) {
-    const int p = j * (kBN / kPage) + qw;
-    const uint32_t id = page_id(p);
+  auto stage_half = [&](int p, uint32_t id, int b, int which) -> StageHalf {
     const int64_t blk = id < nblocks ? id : 0;
-    const char* kp = kbase + blk * block_bytes;
-    const char* vp = vbase + blk * block_bytes;
-    pf_k = kp;
-    pf_v = vp;
-    // LDS byte address of this wave's rows in buffer b (uniform).
-    const uint32_t kd = lds_address(group_lds + b * (KT + VT) + qw * 16 * KROW);
-    const uint32_t vd = kd + KT * sizeof(uint16_t);
-    const uint64_t ks = uniform64(reinterpret_cast<int64_t>(kp));
-    const uint64_t vs = uniform64(reinterpret_cast<int64_t>(vp));
+    const char* src = (which ? vbase : kbase) + blk * block_bytes;
+    return {lds_address(group_lds + b * (KT + VT) + which * KT + qw * 16 * KROW),
+            static_cast<uint64_t>(uniform64(reinterpret_cast<int64_t>(src))), p >= last_page};
+  };
+  auto stage_issue = [&](const StageHalf& h, int i) __attribute__((always_inline)) {
+    lds_dma16(h.dst + i * 4 * KROW * sizeof(uint16_t), h.last ? dma_last[i] : dma_full[i], h.src);
+  };
+  auto issue_half = [&](int p, uint32_t id, int b, int which) __attribute__((always_inline)) {
+    const StageHalf h = stage_half(p, id, b, which);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t off = p >= last_page ? dma_last[i] : dma_full[i];
-      lds_dma16(kd + i * 4 * KROW * sizeof(uint16_t), off, ks);
-      lds_dma16(vd + i * 4 * KROW * sizeof(uint16_t), off, vs);
-    }
+    for (int i = 0; i < 4; ++i) stage_issue(h, i);
+  };
+  // L2 prefetch of page id `id`: lanes 0-31 touch the 32 cache lines of the
+  // wave's K head slices, lanes 32-63 those of V.  Every address stays inside
+  // the page's block.
+  const uint32_t pf_off = static_cast<uint32_t>(((lane & 31) >> 1) * a.kv_token * sizeof(T) + (lane & 1) * 128);
+  auto prefetch_page = [&](uint32_t id) __attribute__((always_inline)) {
+    const int64_t blk = id < nblocks ? id : 0;
+    lds_dma4(lds_address(prefetch_sink + wave * 64), (lane < 32 ? kbase : vbase) + blk * block_bytes + pf_off);
   };
   // Tiles of a key group arrive 2 apart: the group's first tile of chunk c
   // is 16c + kg.
@@ -432,95 +458,61 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // Swizzled layout: a lane's K row is col (+32), its logical chunk 2ks + half;
   // its V rows are rlo and rlo + 8, logical chunk 4c + 2(grp&1) + (gl&3)/2,
   // 8-byte half gl&1 (rows 16ks + r keep r's swizzle).
-  const int kswz = lds_swizzle(col & 15);
-  int v_lo[DTILES], v_hi[DTILES];
-  if constexpr (DMA) {
-    const int rlo = 4 * (grp >> 1) + (gl >> 2);
-    const int m0 = 2 * (grp & 1) + ((gl & 3) >> 1);
-#pragma unroll
-    for (int c = 0; c < DTILES; ++c) {
-      v_lo[c] = rlo * KROW + (((4 * c + m0) ^ lds_swizzle(rlo)) * 8) + 4 * (gl & 1);
-      v_hi[c] = (rlo + 8) * KROW + (((4 * c + m0) ^ lds_swizzle(rlo + 8)) * 8) + 4 * (gl & 1);
-    }
-  }
+  // In bytes, with sw = lds_swizzle(row): chunk (2ks + half) ^ sw of K row
+  // col sits at 32 (ks ^ sw/2) + 16 (half ^ sw%2); V chunk (4c + m0) ^ sw of
+  // rows rlo and rlo + 8 (same swizzle) at 64 (c ^ sw/4) + 16 (m0 ^ sw%4).
+  // So each read is ((step << 5 or 6) ^ key) + base, one v_xad_u32.
+  const int kswz = lds_swizzle(col);
+  const int k_key = (kswz >> 1) << 5;
+  const int k_base = col * KROW * 2 + 16 * (half ^ (kswz & 1));
+  const int rlo = 4 * (grp >> 1) + (gl >> 2);
+  const int m0 = 2 * (grp & 1) + ((gl & 3) >> 1);
+  const int v_key = (lds_swizzle(rlo) >> 2) << 6;
+  const int v_base_lo = rlo * KROW * 2 + 16 * (m0 ^ (lds_swizzle(rlo) & 3)) + 8 * (gl & 1);
+  const int v_base_hi = (rlo + 8) * KROW * 2 + 16 * (m0 ^ (lds_swizzle(rlo + 8) & 3)) + 8 * (gl & 1);
 
   f32x16 acc_o[DTILES];
 #pragma unroll
   for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
-  float m = -INFINITY, lsum = 0.f;
+  float m = -INFINITY;
+  // Row sums of P, accumulated by MFMA against a ones operand: every element
+  // of lane l holds the sum for query column l % 32 (over the rounded P that
+  // also weights V), so the softmax phase spends no vector adds on it.
+  f32x16 acc_l = {};
+  const uint32_t one2 = Ops::pack2(1.f, 1.f);
+  const u32x4 ones = {one2, one2, one2, one2};
 
-  // Per key group, iteration it computes tile j = 2it + kg from buffer it&1
-  // while tile j+2 waits in registers; tile j+2 then goes to the other buffer
-  // (whose tile every wave finished before the previous barrier), and one
-  // barrier per tile publishes it.
-  auto store_tile = [&](int b) {
-    uint16_t* kb = group_lds + b * (KT + VT);
-    uint16_t* vb = kb + KT;
+  // Whether the wave computes tile j: it exists and holds a key visible to
+  // one of the wave's queries.  Once false it stays false for later tiles.
+  auto active = [&](int j) { return j < ntiles && wave_live && j * kBN <= wave_last_key; };
+  // S^T = K Q^T for the tile's two 32-key halves, as two interleaved MFMA
+  // chains (each MFMA has the other chain's MFMA to wait out its K read).
+  auto scores = [&](int b, f32x16 (&sacc)[2]) __attribute__((always_inline)) {
+    const uint16_t* k_lds = group_lds + b * (KT + VT);
+    const int key = DMA ? opaque(k_key) : 0;
+    f32x16 c[2] = {{}, {}};
 #pragma unroll
-    for (int i = 0; i < PASSES; ++i) {
-      const int tok = i * TOKENS_PER_PASS + ld_tok;
-      *reinterpret_cast<u32x4*>(&kb[tok * KROW + ld_chunk * 8]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&vb[tok * VROW + ld_chunk * 8]) = vreg[i];
-    }
+    for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const char* row = reinterpret_cast<const char*>(k_lds + hh * 32 * KROW);
+        const u32x4 kv = DMA ? *reinterpret_cast<const u32x4*>(row + (((ks << 5) ^ key) + k_base))
+                             : *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
+        c[hh] = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c[hh]);
+      }
+    sacc[0] = c[0];
+    sacc[1] = c[1];
   };
-  // Exactly one vector-memory load, the prefetch, follows a tile's staging
-  // loads, so waiting for all but the newest load (vmcnt(1)) completes the
-  // tile's loads while the prefetch stays in flight.  sched_barrier keeps
-  // the prefetch after the staging loads.
-  auto tile_barrier = [&]() { asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
-  if constexpr (DMA) {
-    const int fill = min(4 * ntiles, kTablePages);
-    for (int i = tid; i < fill; i += 512) page_ids[i] = trow[min(i, last_page)];
-    __syncthreads();
-    // The tile of iteration it arrives during iteration it - 1; the barrier
-    // at the top of each iteration (after this wave's staging loads landed)
-    // makes every wave's share visible, and the next tile's loads then go to
-    // the buffer every wave finished reading before that barrier.  The page
-    // two tiles further on is prefetched into L2 meanwhile.
-    if (kg < ntiles) {
-      issue_tile(kg, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      prefetch_tile(kg + 2);
-    }
-  } else {
-    if (kg < ntiles) {
-      load_tile(kg);
-      store_tile(0);
-    }
-    if (kg + 2 < ntiles) load_tile(kg + 2);
-    __syncthreads();
-  }
-  const int niter = (ntiles + 1) / 2;
-  for (int it = 0; it < niter; ++it) {
-    const int j = 2 * it + kg;
-    if constexpr (DMA) {
-      tile_barrier();
-      if (kg < ntiles) {
-        if (j + 2 < ntiles) issue_tile(j + 2, (it + 1) & 1);
-        __builtin_amdgcn_sched_barrier(0);
-        prefetch_tile(j + 4);
-      }
-    }
-    const uint16_t* k_lds = group_lds + (it & 1) * (KT + VT);
-    const uint16_t* v_lds = k_lds + KT;
-    const int key0 = j * kBN;
-    if (j < ntiles && wave_live && key0 <= wave_last_key) {
-    // S^T = K Q^T for the tile's two 32-key halves.
-    f32x16 sacc[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      f32x16 c = {};
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const int kcol = DMA ? (((2 * ks + half) ^ kswz) * 8) : ks * 16 + half * 8;
-        const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + kcol]);
-        c = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c);
-      }
-      sacc[hh] = c;
-    }
-    // Mask (diagonal tiles and the chunk's last rows only) and the tile
-    // maximum of this lane's query.  Element r of half hh holds key
-    // key0 + 32hh + 8(r/4) + 4half + r%4.
+  // Online softmax of tile key0: mask (diagonal tiles and the chunk's last
+  // rows only), tile maximum, exponentials.  Leaves P^T rounded to T as the B
+  // operands of the four 16-key k-steps.  Element r of half hh holds key
+  // key0 + 32hh + 8(r/4) + 4half + r%4.  When the running maximum moves it
+  // returns true with the accumulators' factor in corr; accumulate() applies
+  // it, so acc_o and acc_l change in one place only.  hook(0) .. hook(8) run
+  // at fixed points along the way (the staging loads of the direct-to-LDS
+  // path, spread out so that they never queue up behind one another).
+  auto softmax = [&](int key0, f32x16 (&sacc)[2], u32x4 (&pb)[4], float& corr, auto&& hook)
+                     __attribute__((always_inline)) -> bool {
     float tmax = -INFINITY;
     if (uniform(key0 + kBN - 1 > prefix + wave_row0 || wave_row0 + 31 >= nq)) {
       const int lim = row_valid ? my_key_limit - key0 - 4 * half : -1;
@@ -538,56 +530,189 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[hh][r]);
     }
-    tmax = fmaxf(tmax, xor_lane(tmax, 32)) * a.qscale;
-    if (__builtin_amdgcn_ballot_w64(tmax > m + kRescale)) {
+    hook(0);
+    tmax = max_across_halves(tmax) * a.qscale;
+    hook(1);
+    const bool rescale = __builtin_amdgcn_ballot_w64(tmax > m + kRescale) != 0;
+    if (rescale) {
       const float mn = fmaxf(m, tmax);
-      const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
-      lsum *= corr;
+      corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+      m = mn;
+    }
+    hook(2);
+    // p = 2^(s * scale * log2(e) - m); a lane that has seen no key yet has
+    // only -inf scores, which give 0 against any finite offset.
+    const float mb = (m == -INFINITY) ? 0.f : m;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[hh][r] = fast_exp2(fmaf(sacc[hh][r], a.qscale, -mb));
+        if (r == 5) hook(3 + 3 * hh);
+        if (r == 11) hook(4 + 3 * hh);
+      }
+      if (hh == 0) hook(5);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pb[ks][e] = Ops::pack2(sacc[ks / 2][(ks % 2) * 8 + 2 * e], sacc[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
+    hook(8);
+    return rescale;
+  };
+  // O^T = O^T * corr (when softmax() moved the maximum) + V^T P^T over the
+  // tile's four 16-key k-steps; the row sums likewise.
+  auto accumulate = [&](int b, const u32x4 (&pb)[4], bool rescale, float corr) __attribute__((always_inline)) {
+    if (rescale) {
 #pragma unroll
       for (int c = 0; c < DTILES; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
-      m = mn;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_l[r] *= corr;
     }
-    // p = 2^(s * scale * log2(e) - m); a lane that has seen no key yet has
-    // only -inf scores, which give 0 against any finite offset.
-    const float mb = (m == -INFINITY) ? 0.f : m;
-    float psum = 0.f;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(fmaf(sacc[hh][r], a.qscale, -mb));
-        sacc[hh][r] = p;
-        psum += p;
-      }
-    lsum += psum;
-
-    // O^T += V^T P^T over the tile's four 16-key k-steps.
+    const uint16_t* v_lds = group_lds + b * (KT + VT) + KT;
+    const int key = DMA ? opaque(v_key) : 0;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int hh = ks / 2, base = (ks % 2) * 8;
-      u32x4 pb;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pb[e] = Ops::pack2(sacc[hh][base + 2 * e], sacc[hh][base + 2 * e + 1]);
 #pragma unroll
       for (int c = 0; c < DTILES; ++c) {
-        const uint16_t* vlo = DMA ? &v_lds[v_lo[c] + ks * 16 * VROW] : &v_lds[tr_off + ks * 16 * VROW + c * 32];
-        const uint16_t* vhi = DMA ? &v_lds[v_hi[c] + ks * 16 * VROW] : vlo + 8 * VROW;
+        const char* rows = reinterpret_cast<const char*>(v_lds + ks * 16 * VROW);
+        const uint16_t* vlo = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key) + v_base_lo))
+                                  : &v_lds[tr_off + ks * 16 * VROW + c * 32];
+        const uint16_t* vhi = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key) + v_base_hi))
+                                  : vlo + 8 * VROW;
         const u32x2 lo = lds_read_tr(vlo);
         const u32x2 hi = lds_read_tr(vhi);
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
-        acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
+        acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb[ks]), acc_o[c]);
       }
+      acc_l = Ops::mma(as_v8<V8>(ones), as_v8<V8>(pb[ks]), acc_l);
     }
+  };
+  const int niter = (ntiles + 1) / 2;  // tiles per key group (the last of group 1 may not exist)
+
+  if constexpr (DMA) {
+    const int fill = min(4 * ntiles, kTablePages);
+    for (int i = tid; i < fill; i += 512) page_ids[i] = trow[min(i, last_page)];
+    __syncthreads();
+    // Ping-pong.  Iteration t of key group g handles tile j = 2t + g in two
+    // phases: an MFMA phase (P V of tile j - 2, then S of tile j) and a
+    // softmax phase (tile j's exponentials, with the staging DMA of K of tile
+    // j + 4 and V of tile j + 2 into the buffers the MFMA phase just finished
+    // reading, and an L2 prefetch of tile j + 6, issued one instruction at a
+    // time between the softmax's steps).  Group 1 runs one phase behind group
+    // 0 and every phase ends at a workgroup barrier, so on each SIMD one wave
+    // issues MFMAs while its partner (same query rows, other key group) runs
+    // the softmax and the loads.  Both groups pass 2 * niter + 2 barriers.
+    //
+    // Loads: every softmax phase issues exactly 9 (4 K, 4 V, then the
+    // prefetch; past the last tile they re-read it into buffers no later
+    // phase reads), so at the barrier before MFMA phase t, vmcnt(9) completes
+    // everything issued before the previous softmax phase -- the K of tile j
+    // and V of tile j - 2 that this phase reads (loads return in order).  The
+    // prologue issues K(j), V(j), K(j + 2) and a prefetch: vmcnt(9) there
+    // completes K(j).  Page ids run down a chain (V <- K <- prefetch), so each
+    // phase reads one new id from LDS, a phase before its use.
+    auto load_barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto phase_barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    issue_half(tile_page(kg), page_id(tile_page(kg)), 0, 0);
+    issue_half(tile_page(kg), page_id(tile_page(kg)), 0, 1);
+    issue_half(tile_page(kg + 2), page_id(tile_page(kg + 2)), 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch_page(page_id(tile_page(kg + 4)));
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t id_v = page_id(tile_page(kg + 2));       // V of tile j + 2
+    uint32_t id_k = page_id(tile_page(kg + 4));       // K of tile j + 4
+    int32_t next_pf = page_slot(tile_page(kg + 6));   // prefetch of tile j + 6
+    if (kg == 1) phase_barrier();
+    f32x16 sacc[2];
+    u32x4 pb[4];
+    bool rescale = false;
+    float corr = 1.f;
+    for (int t = 0; t <= niter; ++t) {
+      const int j = 2 * t + kg;
+      const int P = t & 1;
+      load_barrier();
+      __builtin_amdgcn_s_setprio(1);
+      // One site each for P V and S: accumulators updated on two paths
+      // would be given two register sets.
+      if (t >= 1 && active(j - 2)) accumulate(1 - P, pb, rescale, corr);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t < niter && active(j)) scores(P, sacc);
+      __builtin_amdgcn_s_setprio(0);
+      if (t == niter) break;
+      phase_barrier();
+      const uint32_t id_pf = static_cast<uint32_t>(uniform(next_pf));
+      next_pf = page_slot(tile_page(j + 8));
+      const StageHalf hk = stage_half(tile_page(j + 4), id_k, P, 0);
+      const StageHalf hv = stage_half(tile_page(j + 2), id_v, 1 - P, 1);
+      auto stage = [&](int n) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (n < 4) stage_issue(hk, n);
+        else if (n < 8) stage_issue(hv, n - 4);
+        else prefetch_page(id_pf);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      if (active(j)) {
+        rescale = softmax(j * kBN, sacc, pb, corr, stage);
+      } else {
+#pragma unroll
+        for (int n = 0; n < 9; ++n) stage(n);
+      }
+      id_v = id_k;
+      id_k = id_pf;
     }
-    if constexpr (!DMA) {
+    if (kg == 0) phase_barrier();
+    // Every staging load has landed and every tile read is done before the
+    // merge reuses LDS.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  } else {
+    // Iteration it computes tile j = 2it + kg from buffer it&1 while tile
+    // j + 2 waits in registers; tile j + 2 then goes to the other buffer
+    // (whose tile every wave finished before the previous barrier), and one
+    // barrier per tile publishes it.
+    auto store_tile = [&](int b) {
+      uint16_t* kb = group_lds + b * (KT + VT);
+      uint16_t* vb = kb + KT;
+#pragma unroll
+      for (int i = 0; i < PASSES; ++i) {
+        const int tok = i * TOKENS_PER_PASS + ld_tok;
+        *reinterpret_cast<u32x4*>(&kb[tok * KROW + ld_chunk * 8]) = kreg[i];
+        *reinterpret_cast<u32x4*>(&vb[tok * VROW + ld_chunk * 8]) = vreg[i];
+      }
+    };
+    if (kg < ntiles) {
+      load_tile(kg);
+      store_tile(0);
+    }
+    if (kg + 2 < ntiles) load_tile(kg + 2);
+    __syncthreads();
+    for (int it = 0; it < niter; ++it) {
+      const int j = 2 * it + kg;
+      if (active(j)) {
+        f32x16 sacc[2];
+        u32x4 pb[4];
+        float corr = 1.f;
+        scores(it & 1, sacc);
+        const bool rescale = softmax(j * kBN, sacc, pb, corr, [](int) {});
+        accumulate(it & 1, pb, rescale, corr);
+      }
       if (j + 2 < ntiles) store_tile((it + 1) & 1);
       __syncthreads();
       if (j + 4 < ntiles) load_tile(j + 4);
     }
   }
-  if constexpr (DMA) __syncthreads();  // every tile read before the merge reuses LDS
 
   // Merge the key groups: group 1 hands (m, l, acc) to group 0 through LDS,
   // laid out [query wave][value][lane] (the last barrier ordered every tile
@@ -595,7 +720,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   float* xs = reinterpret_cast<float*>(lds) + qw * MERGE_FLOATS * 64 + lane;
   if (kg == 1) {
     xs[0] = m;
-    xs[64] = lsum;
+    xs[64] = acc_l[0];
 #pragma unroll
     for (int c = 0; c < DTILES; ++c)
 #pragma unroll
@@ -603,19 +728,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   __syncthreads();
   if (kg == 1) return;
+  float total;  // the row's sum of P
   {
     const float m1 = xs[0];
     const float mm = fmaxf(m, m1);
     const float c0 = (m == -INFINITY) ? 0.f : fast_exp2(m - mm);
     const float c1 = (m1 == -INFINITY) ? 0.f : fast_exp2(m1 - mm);
-    lsum = lsum * c0 + xs[64] * c1;
+    total = acc_l[0] * c0 + xs[64] * c1;
 #pragma unroll
     for (int c = 0; c < DTILES; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc_o[c][r] = acc_o[c][r] * c0 + xs[(2 + c * 16 + r) * 64] * c1;
   }
 
-  const float total = lsum + xor_lane(lsum, 32);
   if (!wave_live || !row_valid) return;
   const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key is written as zeros
   T* orow = static_cast<T*>(a.out) + (row0 + my_row) * a.o_row + static_cast<int64_t>(h) * a.o_head;
