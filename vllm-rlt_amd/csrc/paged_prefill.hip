@@ -103,14 +103,20 @@ __device__ __forceinline__ uint32_t lds_address(P* p) {
 }
 
 // Position of logical 16-byte chunk c of LDS row r (256 bytes) is
-// c ^ lds_swizzle(r).  The 32 banks span 128 bytes, i.e. 8 chunk positions,
-// and a 16-byte read serves 8 consecutive lanes per pass: since the swizzle's
-// low 3 bits are a bijection of r % 8, 8 consecutive rows put one logical
-// chunk in 8 distinct bank groups (the K reads).  An 8-byte read serves 16
-// lanes per pass; bits 1-2 are a bijection of r % 4, so 4 consecutive rows
-// from a multiple of 4 put an aligned chunk pair in 4 distinct 32-byte
-// groups (the transposing V reads).  Rows r and r + 8 share a swizzle.
-__device__ __forceinline__ int lds_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// c ^ lds_swizzle(r), with swizzle bits (b0, b1, b2, b3) = (r2, r0, r1,
+// r0 ^ r1 ^ r3).  Its 4 bits are a bijection of r % 16 and its low 3 bits one
+// of r % 8, so 16 (or 8) consecutive rows put one logical chunk in distinct
+// 16-byte bank groups: the K reads (16 bytes per lane, one row per lane) are
+// conflict-free whether a pass serves 16 lanes over 256 bytes of banks or 8
+// lanes over 128.  Bits 1-2 and bits 2-3 are each a bijection of r % 4, so
+// 4 consecutive rows from a multiple of 4 put an aligned chunk pair, and an
+// aligned chunk quad, in distinct bank groups: the transposing V reads (4
+// rows x 32 or 64 bytes per pass) are conflict-free too.  (Simpler swizzles
+// that satisfy only one of the two bank models measure bank-conflict cycles
+// on gfx950; this one measures none.)
+__device__ __forceinline__ int lds_swizzle(int r) {
+  return ((r >> 2) & 1) | ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r ^ (r >> 1) ^ (r >> 3)) & 1) << 3);
+}
 
 // x, as a value the compiler cannot see through: addresses derived from it
 // are recomputed where they are used (a few integer operations) instead of
@@ -460,7 +466,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // 8-byte half gl&1 (rows 16ks + r keep r's swizzle).
   // In bytes, with sw = lds_swizzle(row): chunk (2ks + half) ^ sw of K row
   // col sits at 32 (ks ^ sw/2) + 16 (half ^ sw%2); V chunk (4c + m0) ^ sw of
-  // rows rlo and rlo + 8 (same swizzle) at 64 (c ^ sw/4) + 16 (m0 ^ sw%4).
+  // row rlo (and likewise rlo + 8, with its own swizzle) at 64 (c ^ sw/4) +
+  // 16 (m0 ^ sw%4).
   // So each read is ((step << 5 or 6) ^ key) + base, one v_xad_u32.
   const int kswz = lds_swizzle(col);
   const int k_key = (kswz >> 1) << 5;
@@ -468,6 +475,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int rlo = 4 * (grp >> 1) + (gl >> 2);
   const int m0 = 2 * (grp & 1) + ((gl & 3) >> 1);
   const int v_key = (lds_swizzle(rlo) >> 2) << 6;
+  const int v_key_hi = (lds_swizzle(rlo + 8) >> 2) << 6;
   const int v_base_lo = rlo * KROW * 2 + 16 * (m0 ^ (lds_swizzle(rlo) & 3)) + 8 * (gl & 1);
   const int v_base_hi = (rlo + 8) * KROW * 2 + 16 * (m0 ^ (lds_swizzle(rlo + 8) & 3)) + 8 * (gl & 1);
 
@@ -574,6 +582,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
     const uint16_t* v_lds = group_lds + b * (KT + VT) + KT;
     const int key = DMA ? opaque(v_key) : 0;
+    const int key_hi = DMA ? opaque(v_key_hi) : 0;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
@@ -581,7 +590,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         const char* rows = reinterpret_cast<const char*>(v_lds + ks * 16 * VROW);
         const uint16_t* vlo = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key) + v_base_lo))
                                   : &v_lds[tr_off + ks * 16 * VROW + c * 32];
-        const uint16_t* vhi = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key) + v_base_hi))
+        const uint16_t* vhi = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key_hi) + v_base_hi))
                                   : vlo + 8 * VROW;
         const u32x2 lo = lds_read_tr(vlo);
         const u32x2 hi = lds_read_tr(vhi);
