@@ -174,35 +174,49 @@ __device__ __forceinline__ int find_row(const int* prefix, int n, int x) {
 
 // Merges the ns >= 2 split partials of (row r, kv head h) into the output.
 // Lane sp holds split sp's (max, sum) (kMaxSplits == 64 == wave size), so the
-// global max and the normaliser are two wave reductions; each dim's
-// accumulator is summed over splits in split order, loads issued eight at a
-// time.  The result depends only on the row's own partials.
-template <typename T>
+// global max and the normaliser are two wave reductions; lane l sums dims
+// l, l + 64, ... over splits in split order.  The accumulator loads do not
+// depend on the reductions, so the first batch (all of the lane's dims for up
+// to 64 / (D / 64) splits) is issued together with the (max, sum) load: one
+// round trip to memory for the common split counts instead of one per eight
+// splits.  The result depends only on the row's own partials.
+template <typename T, int D>
 __device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int lane) {
   static_assert(kMaxSplits == 64, "one lane per split");
+  static_assert(D % 64 == 0 && D <= 256, "dims per lane");
+  constexpr int DPL = D / 64;      // dims per lane
+  constexpr int SPB = 64 / DPL;    // splits per load batch
   const int G = a.hq / a.hkv;
   const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
+  const int64_t split_stride = static_cast<int64_t>(G) * D;
   for (int j = 0; j < G; ++j) {
     T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
+    const float* base = a.ws_acc + (slot0 * G + j) * D + lane;
     const float2 ml = lane < ns ? a.ws_ml[(slot0 + lane) * G + j] : make_float2(-INFINITY, 0.f);
+    float x[DPL][SPB];
+#pragma unroll
+    for (int u = 0; u < SPB; ++u)
+#pragma unroll
+      for (int dd = 0; dd < DPL; ++dd) x[dd][u] = u < ns ? base[u * split_stride + dd * 64] : 0.f;
     const float M = strided_max<1>(ml.x);
     const float w = lane < ns ? fast_exp2(ml.x - M) : 0.f;
     const float inv = 1.f / group_sum<64>(ml.y * w);
-    const float* base = a.ws_acc + (slot0 * G + j) * a.d;
-    const int64_t split_stride = static_cast<int64_t>(G) * a.d;
-    for (int d = lane; d < a.d; d += 64) {
-      float acc = 0.f;
-      int sp = 0;
-      for (; sp + 8 <= ns; sp += 8) {
-        float x[8];
+    float acc[DPL];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = base[(sp + u) * split_stride + d];
+    for (int dd = 0; dd < DPL; ++dd) acc[dd] = 0.f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = fmaf(x[u], __shfl(w, sp + u, 64), acc);
-      }
-      for (; sp < ns; ++sp) acc = fmaf(base[sp * split_stride + d], __shfl(w, sp, 64), acc);
-      store_elem(orow + d * a.o_dim, acc * inv);
+    for (int u = 0; u < SPB; ++u) {
+      const float wu = __shfl(w, u, 64);
+#pragma unroll
+      for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(x[dd][u], wu, acc[dd]);
     }
+    for (int sp = SPB; sp < ns; ++sp) {
+      const float wu = __shfl(w, sp, 64);
+#pragma unroll
+      for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(base[sp * split_stride + dd * 64], wu, acc[dd]);
+    }
+#pragma unroll
+    for (int dd = 0; dd < DPL; ++dd) store_elem(orow + (lane + dd * 64) * a.o_dim, acc[dd] * inv);
   }
 }
 
@@ -458,7 +472,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 }
 
 // Merge kernel: one wavefront per (row, kv_head) with more than one split.
-template <typename T>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (item >= a.n_rows * a.hkv) return;
@@ -466,7 +480,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int h = item - r * a.hkv;
   int split_len, ns;
   split_plan(row_length(a, r), &split_len, &ns);
-  if (ns > 1) merge_partials<T>(a, r, h, ns, threadIdx.x & 63);
+  if (ns > 1) merge_partials<T, D>(a, r, h, ns, threadIdx.x & 63);
 }
 
 // Generic kernel for shapes the tiled kernel does not cover (odd head_dim,
@@ -617,7 +631,10 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   }
   if (int rc = check_launch("rlt_paged_decode")) return rc;
   const int merge_grid = (a.n_rows * a.hkv + kWaves - 1) / kWaves;
-  hipLaunchKernelGGL(paged_decode_merge_kernel<T>, dim3(merge_grid), dim3(64 * kWaves), 0, stream, a);
+  const dim3 mgrid(merge_grid), mblock(64 * kWaves);
+  if (a.d == 64) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 64>), mgrid, mblock, 0, stream, a);
+  else if (a.d == 128) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 128>), mgrid, mblock, 0, stream, a);
+  else hipLaunchKernelGGL((paged_decode_merge_kernel<T, 256>), mgrid, mblock, 0, stream, a);
   return check_launch("rlt_paged_decode(merge)");
 }
 
