@@ -311,3 +311,33 @@ def test_mfma_prefill_negative_scale_negates_scores(d):
     torch.testing.assert_close(out.cpu(), expect, atol=2e-2, rtol=1e-2)
     with pytest.raises(ValueError, match="scale"):
         ops.paged_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), cu.cuda(), 129, scale=0.0)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_mfma_prefill_random_shapes(seed):
+    # Seeded random packed batches: odd and even key-tile counts (the second key
+    # group's last tile may not exist), one-tile workgroups, chunks shorter
+    # than a wave's rows (waves wholly past the chunk), diagonal tiles at every
+    # offset, GQA, both dtypes and head sizes, ranked and direct work lists.
+    from vllm_rlt_amd import ops
+
+    g = torch.Generator().manual_seed(1000 + seed)
+    n = int(torch.randint(1, 6, (1,), generator=g))
+    prefixes = [int(x) for x in torch.randint(0, 700, (n,), generator=g)]
+    chunks = [int(x) for x in torch.randint(1, 300, (n,), generator=g)]
+    if seed % 3 == 0:
+        prefixes[0] = 0  # a chunk over an empty prefix
+    if seed % 4 == 1:
+        chunks[-1] = 64 * int(torch.randint(1, 4, (1,), generator=g))  # chunk ending on a tile edge
+    hq, hkv = [(16, 16), (8, 2), (4, 4), (16, 4)][seed % 4]
+    d = 64 if seed % 5 == 4 else 128
+    dtype = torch.float16 if seed % 2 else torch.bfloat16
+    q, kp, vp, tables, lens, cu, row_tables, row_lengths = ragged_prefill_case(
+        dtype, hq, hkv, d, prefixes, chunks, seed
+    )
+    print(f"[prefill random] seed={seed} prefixes={prefixes} chunks={chunks} hq={hq} hkv={hkv} d={d} {dtype}", flush=True)
+    out = ops.paged_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), cu.cuda(), max(chunks))
+    torch.cuda.synchronize()
+    expect = paged_attention_cpu(q, kp, vp, row_tables, row_lengths)
+    atol, rtol = TOL[dtype]
+    torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
