@@ -210,10 +210,18 @@ __device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int la
 #pragma unroll
       for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(x[dd][u], wu, acc[dd]);
     }
-    for (int sp = SPB; sp < ns; ++sp) {
-      const float wu = __shfl(w, sp, 64);
+    // Further splits (long rows), a whole batch of loads in flight at a time.
+    for (int sp0 = SPB; sp0 < ns; sp0 += SPB) {
 #pragma unroll
-      for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(base[sp * split_stride + dd * 64], wu, acc[dd]);
+      for (int u = 0; u < SPB; ++u)
+#pragma unroll
+        for (int dd = 0; dd < DPL; ++dd) x[dd][u] = sp0 + u < ns ? base[(sp0 + u) * split_stride + dd * 64] : 0.f;
+#pragma unroll
+      for (int u = 0; u < SPB; ++u) {
+        const float wu = __shfl(w, (sp0 + u) & 63, 64);
+#pragma unroll
+        for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(x[dd][u], wu, acc[dd]);
+      }
     }
 #pragma unroll
     for (int dd = 0; dd < DPL; ++dd) store_elem(orow + (lane + dd * 64) * a.o_dim, acc[dd] * inv);
