@@ -385,6 +385,12 @@ def spot_check(w):
     return err
 
 
+def iqr(values):
+    """[25th, 75th] percentile of the values (ms), rounded."""
+    q = statistics.quantiles(values, n=4) if len(values) > 1 else [values[0]] * 3
+    return [round(q[0], 5), round(q[2], 5)]
+
+
 def cpu_baseline(w, step, reps):
     """The CPU oracle (op-for-op restatement of the reference CPU path) on one layer-step.
 
@@ -410,20 +416,28 @@ def cpu_baseline(w, step, reps):
     blocks = remap[w.blocks.cpu()]
     offsets = w.offsets.cpu()
     q, k_new, v_new = w.q[0].cpu(), w.k_new[0].cpu(), w.v_new[0].cpu()
-    times = []
-    for _ in range(reps + 1):
-        t0 = time.perf_counter()
-        kv_ops.append(kc, vc, 0, blocks, offsets, k_new, v_new)
-        paged_attention_cpu(q, kc[:, 0], vc[:, 0], local, lengths)
-        times.append(time.perf_counter() - t0)
-    layer_s = statistics.median(times[1:])
+    def layer_time(reps):
+        times = []
+        for _ in range(reps + 1):
+            t0 = time.perf_counter()
+            kv_ops.append(kc, vc, 0, blocks, offsets, k_new, v_new)
+            paged_attention_cpu(q, kc[:, 0], vc[:, 0], local, lengths)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times[1:])
+
+    layer_s = layer_time(reps)
+    torch.set_num_threads(1)
+    single_s = layer_time(1)
+    torch.set_num_threads(threads)
     return {
         "value": 1.0 / (LAYERS * layer_s),
         "unit": "loop-steps/s",
         "cores": threads,
         "kind": "port",
+        "single_thread_value": 1.0 / (LAYERS * single_s),
         "sample": f"one layer-step (all {w.batch} rows, 1 layer, append + attention), median of {reps} "
-        f"after 1 warmup, extrapolated x{LAYERS} layers; {layer_s * 1e3:.1f} ms/layer-step; "
+        f"after 1 warmup, extrapolated x{LAYERS} layers; {layer_s * 1e3:.1f} ms/layer-step on {threads} "
+        f"threads, {single_s * 1e3:.1f} ms on 1 thread (1 run after 1 warmup); "
         f"cpu={platform.processor() or platform.machine()}",
     }
 
@@ -523,6 +537,62 @@ def prefill_spot_check(w):
     return worst
 
 
+def prefill_cpu_baseline(w, reps, stride=32):
+    """The per-token CPU oracle on a bounded sample of the prefill launch.
+
+    Sample: every `stride`-th query row of every chunk at depth 0, layer 0 (each
+    row attends over its own causal length), against a 1-layer host copy of the
+    pages those sequences reference.  TFLOP/s = the sampled rows' algorithmic
+    FLOPs / median time, comparable with the kernel's per-launch rate.
+    """
+    from oracle.paged_attention import paged_attention_cpu
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    chunk = PREFILL["chunk"]
+    tables = w.depth_tables[0].cpu()
+    lens = w.lens
+    need = sorted({int(b) for s in range(len(lens)) for b in tables[s, : math.ceil(int(lens[s]) / PAGE)]})
+    remap = torch.full((w.num_blocks,), -1, dtype=torch.int64)
+    remap[torch.tensor(need)] = torch.arange(len(need))
+    idx = torch.tensor(need, device=w.key_cache.device)
+    kc = w.key_cache[idx, 0].cpu()  # [used blocks, page, hkv, d]
+    vc = w.value_cache[idx, 0].cpu()
+    rows, row_lens, row_seq = [], [], []
+    for s in range(len(lens)):
+        for i in range(0, chunk, stride):
+            rows.append(s * chunk + i)
+            row_lens.append(int(w.prefixes[s]) + i + 1)
+            row_seq.append(s)
+    local = torch.where(tables >= 0, remap[tables.clamp_min(0).long()], -1).to(torch.int32)[row_seq]
+    q = w.q[0][rows].cpu()
+    lengths = torch.tensor(row_lens, dtype=torch.int32)
+
+    def timed(reps):
+        times = []
+        for _ in range(reps + 1):
+            t0 = time.perf_counter()
+            paged_attention_cpu(q, kc, vc, local, lengths)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times[1:])
+
+    t_multi = timed(reps)
+    torch.set_num_threads(1)
+    t_single = timed(1)
+    torch.set_num_threads(threads)
+    flops = 4 * HQ * HEAD_DIM * sum(row_lens)
+    return {
+        "value": flops / t_multi / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "single_thread_value": flops / t_single / 1e12,
+        "sample": f"{len(rows)} query rows (1 in {stride} of each 512-token chunk, depth 0, layer 0, "
+        f"{sum(row_lens)} visible keys), median of {reps} after 1 warmup: {t_multi * 1e3:.1f} ms on {threads} "
+        f"threads, {t_single * 1e3:.1f} ms on 1 thread; cpu={platform.processor() or platform.machine()}",
+    }
+
+
 def run_prefill(args, device):
     t_setup = time.perf_counter()
     w = PrefillWorkload(args.seed, device)
@@ -553,7 +623,8 @@ def run_prefill(args, device):
                 w.layer(depth, layer, ev)
                 pairs.append(ev)
     torch.cuda.synchronize()
-    launch_ms = statistics.fmean(a.elapsed_time(b) for a, b in pairs)
+    launch_list = [a.elapsed_time(b) for a, b in pairs]
+    launch_ms = statistics.fmean(launch_list)
     flops = w.flops()
     launch_tflops = flops / (LOOPS * LAYERS) / (launch_ms * 1e-3) / 1e12
     step_tflops = flops * args.steps / elapsed / 1e12
@@ -587,9 +658,14 @@ def run_prefill(args, device):
             "frac": round(launch_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": profiled_traffic("ouro-prefill"),
             "avg_launch_ms": round(launch_ms, 5),
+            "median_launch_ms": round(statistics.median(launch_list), 5),
+            "launch_ms_iqr": iqr(launch_list),
             "algorithmic_flops_per_launch": int(flops / (LOOPS * LAYERS)),
         },
     }
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = prefill_cpu_baseline(w, args.cpu_reps)
     print(json.dumps(line), flush=True)
 
 
@@ -654,16 +730,21 @@ def main():
             static.copy_(w.descriptors[step])
             graph.replay()
     torch.cuda.synchronize()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
+    marks[0].record()
     if graph is None:
-        for step in range(args.warmup, total):
+        for i, step in enumerate(range(args.warmup, total)):
             loop_step(w, step)
+            marks[i + 1].record()
     else:
-        for step in range(args.warmup, total):
+        for i, step in enumerate(range(args.warmup, total)):
             static.copy_(w.descriptors[step])
             graph.replay()
+            marks[i + 1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    step_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
     if graph is not None:
         # The replayed steps must leave the same outputs as eager steps.
         last = w.out.clone()
@@ -691,7 +772,8 @@ def main():
             end.record(stream)
             pairs.append((start, end))
     torch.cuda.synchronize()
-    decode_ms = statistics.fmean(s.elapsed_time(e) for s, e in pairs)
+    launch_ms = [s.elapsed_time(e) for s, e in pairs]
+    decode_ms = statistics.fmean(launch_ms)
     decode_avg_bytes = statistics.fmean(decode_bytes)
     unique_avg_bytes = statistics.fmean(unique_bytes)
     # Aliased prefix pages are read by every row but fetched from HBM about
@@ -727,6 +809,8 @@ def main():
         },
         "hbm_gb_per_s": round(gbs, 1),
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "step_ms_median": round(statistics.median(step_ms), 4),
+        "step_ms_iqr": iqr(step_ms),
         "roofline": {
             "kernel": "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)",
             "bound": "hbm",
@@ -736,6 +820,8 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(args.workload),
             "avg_launch_ms": round(decode_ms, 5),
+            "median_launch_ms": round(statistics.median(launch_ms), 5),
+            "launch_ms_iqr": iqr(launch_ms),
             "algorithmic_bytes_per_launch": int(unique_avg_bytes),
         },
     }
