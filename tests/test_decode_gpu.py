@@ -48,6 +48,14 @@ def test_tiled_decode_matches_oracle(dtype, hq, hkv):
     assert_close(run_hip(case), case)
 
 
+@pytest.mark.parametrize("d", [128, 256])
+def test_tiled_decode_long_rows_many_splits(d):
+    # 33 to 65 splits per row: the merge's further load batches (beyond the first
+    # 64 / (d / 64) splits) and the doubled split length past 64 splits.
+    case = random_decode_case([8449, 12000, 16640, 300, 0], hq=4, hkv=4, d=d, dtype=torch.bfloat16, seed=d + 5)
+    assert_close(run_hip(case), case)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [64, 256])
 def test_tiled_decode_other_head_dims(dtype, d):
