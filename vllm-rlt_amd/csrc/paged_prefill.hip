@@ -83,16 +83,12 @@ typedef __attribute__((address_space(1))) void global_void;
 // compiler's wait analysis, which cannot tell the tile buffers apart, does not
 // wait for a tile still in flight before reading the previous one: the
 // kernel orders them itself with explicit vmcnt waits and barriers.  Lane l
-// writes bytes [l*16, l*16 + 16) (dword form: [l*4, l*4 + 4)) after the LDS
-// byte address in M0.  The kernel uses M0 for nothing else.
+// writes bytes [l*16, l*16 + 16) after the LDS byte address in M0.  The
+// kernel uses M0 for nothing else.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(uint32_t lds_byte, uint32_t offset, uint64_t base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_byte), "v"(offset), "s"(base)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma4(uint32_t lds_byte, const void* address) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_byte), "v"(address)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -255,8 +251,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // Two key groups, each with two K and V tile buffers; reused for ranking
   // before the tile loop and for the key-group merge after it.
   __shared__ __align__(16) uint16_t lds[4 * (KT + VT)];
-  // Landing area of the L2 prefetches (never read): one dword per lane.
-  __shared__ __align__(16) uint32_t prefetch_sink[DMA ? 8 * 64 : 1];
   // Page ids of the workgroup's key range (direct-to-LDS path), staged once so
   // that the tile loop reads them from LDS rather than global memory.
   __shared__ int32_t page_ids[DMA ? kTablePages : 1];
@@ -430,14 +424,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
     for (int i = 0; i < 4; ++i) stage_issue(h, i);
   };
-  // L2 prefetch of page id `id`: lanes 0-31 touch the 32 cache lines of the
-  // wave's K head slices, lanes 32-63 those of V.  Every address stays inside
-  // the page's block.
-  const uint32_t pf_off = static_cast<uint32_t>(((lane & 31) >> 1) * a.kv_token * sizeof(T) + (lane & 1) * 128);
-  auto prefetch_page = [&](uint32_t id) __attribute__((always_inline)) {
-    const int64_t blk = id < nblocks ? id : 0;
-    lds_dma4(lds_address(prefetch_sink + wave * 64), (lane < 32 ? kbase : vbase) + blk * block_bytes + pf_off);
-  };
   // Tiles of a key group arrive 2 apart: the group's first tile of chunk c
   // is 16c + kg.
   auto load_tile = [&](int j) {
@@ -516,7 +502,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // operands of the four 16-key k-steps.  Element r of half hh holds key
   // key0 + 32hh + 8(r/4) + 4half + r%4.  When the running maximum moves it
   // returns true with the accumulators' factor in corr; accumulate() applies
-  // it, so acc_o and acc_l change in one place only.  hook(0) .. hook(8) run
+  // it, so acc_o and acc_l change in one place only.  hook(0) .. hook(7) run
   // at fixed points along the way (the staging loads of the direct-to-LDS
   // path, spread out so that they never queue up behind one another).
   auto softmax = [&](int key0, f32x16 (&sacc)[2], u32x4 (&pb)[4], float& corr, auto&& hook)
@@ -566,7 +552,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         pb[ks][e] = Ops::pack2(sacc[ks / 2][(ks % 2) * 8 + 2 * e], sacc[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
-    hook(8);
     return rescale;
   };
   // O^T = O^T * corr (when softmax() moved the maximum) + V^T P^T over the
@@ -610,23 +595,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     // phases: an MFMA phase (P V of tile j - 2, then S of tile j) and a
     // softmax phase (tile j's exponentials, with the staging DMA of K of tile
     // j + 4 and V of tile j + 2 into the buffers the MFMA phase just finished
-    // reading, and an L2 prefetch of tile j + 6, issued one instruction at a
-    // time between the softmax's steps).  Group 1 runs one phase behind group
-    // 0 and every phase ends at a workgroup barrier, so on each SIMD one wave
-    // issues MFMAs while its partner (same query rows, other key group) runs
-    // the softmax and the loads.  Both groups pass 2 * niter + 2 barriers.
+    // reading, issued one instruction at a time between the softmax's steps).
+    // Group 1 runs one phase behind group 0 and every phase ends at a
+    // workgroup barrier, so on each SIMD one wave issues MFMAs while its
+    // partner (same query rows, other key group) runs the softmax and the
+    // loads.  Both groups pass 2 * niter + 2 barriers.
     //
-    // Loads: every softmax phase issues exactly 9 (4 K, 4 V, then the
-    // prefetch; past the last tile they re-read it into buffers no later
-    // phase reads), so at the barrier before MFMA phase t, vmcnt(9) completes
-    // everything issued before the previous softmax phase -- the K of tile j
-    // and V of tile j - 2 that this phase reads (loads return in order).  The
-    // prologue issues K(j), V(j), K(j + 2) and a prefetch: vmcnt(9) there
-    // completes K(j).  Page ids run down a chain (V <- K <- prefetch), so each
-    // phase reads one new id from LDS, a phase before its use.
+    // Loads: every softmax phase issues exactly 8 (4 K, then 4 V; past the
+    // last tile they re-read it into buffers no later phase reads), so at the
+    // barrier before MFMA phase t, vmcnt(8) completes everything issued
+    // before the previous softmax phase -- the K of tile j and V of tile j - 2
+    // that this phase reads (loads return in order).  The prologue issues
+    // K(j), V(j), K(j + 2): vmcnt(8) there completes K(j).  Page ids run down
+    // a chain (V <- K <- next), so each phase reads one new id from LDS, a
+    // phase before its use.  No load here is a bare L2 prefetch of a later
+    // tile: with in-order completion, the barrier's vmcnt would wait for its
+    // HBM latency (a prefetch of tile j + 6 measured 8% slower overall).
     auto load_barrier = [&]() {
       __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     };
     auto phase_barrier = [&]() {
@@ -638,11 +625,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     issue_half(tile_page(kg), page_id(tile_page(kg)), 0, 1);
     issue_half(tile_page(kg + 2), page_id(tile_page(kg + 2)), 1, 0);
     __builtin_amdgcn_sched_barrier(0);
-    prefetch_page(page_id(tile_page(kg + 4)));
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t id_v = page_id(tile_page(kg + 2));       // V of tile j + 2
-    uint32_t id_k = page_id(tile_page(kg + 4));       // K of tile j + 4
-    int32_t next_pf = page_slot(tile_page(kg + 6));   // prefetch of tile j + 6
+    uint32_t id_v = page_id(tile_page(kg + 2));        // V of tile j + 2
+    uint32_t id_k = page_id(tile_page(kg + 4));        // K of tile j + 4
+    int32_t next_k = page_slot(tile_page(kg + 6));     // K of tile j + 6
     if (kg == 1) phase_barrier();
     f32x16 sacc[2];
     u32x4 pb[4];
@@ -661,25 +646,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       __builtin_amdgcn_s_setprio(0);
       if (t == niter) break;
       phase_barrier();
-      const uint32_t id_pf = static_cast<uint32_t>(uniform(next_pf));
-      next_pf = page_slot(tile_page(j + 8));
+      const uint32_t id_next = static_cast<uint32_t>(uniform(next_k));
+      next_k = page_slot(tile_page(j + 8));
       const StageHalf hk = stage_half(tile_page(j + 4), id_k, P, 0);
       const StageHalf hv = stage_half(tile_page(j + 2), id_v, 1 - P, 1);
       auto stage = [&](int n) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
         if (n < 4) stage_issue(hk, n);
-        else if (n < 8) stage_issue(hv, n - 4);
-        else prefetch_page(id_pf);
+        else stage_issue(hv, n - 4);
         __builtin_amdgcn_sched_barrier(0);
       };
       if (active(j)) {
         rescale = softmax(j * kBN, sacc, pb, corr, stage);
       } else {
 #pragma unroll
-        for (int n = 0; n < 9; ++n) stage(n);
+        for (int n = 0; n < 8; ++n) stage(n);
       }
       id_v = id_k;
-      id_k = id_pf;
+      id_k = id_next;
     }
     if (kg == 0) phase_barrier();
     // Every staging load has landed and every tile read is done before the
