@@ -7,11 +7,13 @@ include/rlt_kv.h).
 
 from . import ops
 from .async_state import AsyncState, RoutingBank
+from .buffers import Workspace
 from .device_cache import DeviceCache
 from .graphs import RecurrentGraphs
 from .kv_cache_manager import KVCacheManager
 from .page_book import KVPageBook, PreparedKVBatch
 from .paged_attention import HipPagedAttention, hip_paged_attention
+from .prefill_metadata import PrefillMetadataBank
 
 __all__ = [
     "AsyncState",
@@ -19,9 +21,11 @@ __all__ = [
     "HipPagedAttention",
     "KVCacheManager",
     "KVPageBook",
+    "PrefillMetadataBank",
     "PreparedKVBatch",
     "RecurrentGraphs",
     "RoutingBank",
+    "Workspace",
     "hip_paged_attention",
     "ops",
 ]
