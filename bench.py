@@ -280,6 +280,13 @@ class Workload:
         self.workspace = torch.empty(
             ops.decode_workspace_bytes(n, HQ, HKV, HEAD_DIM), dtype=torch.uint8, device=device
         )
+        # Every row's table begins with the aliased prefix pages: the decode reads
+        # them once per launch for all rows (rlt_paged_decode_shared_prefix).
+        self.prefix_hint = None
+        if self.shared_pages.numel():
+            self.prefix_hint = ops.shared_prefix(
+                range(n), self.shared_pages, n, [int(c) for c in self.contexts], device
+            )
 
     def lengths_at(self, step):
         """Attention length of every row at a step (context incl. the appended token)."""
@@ -315,7 +322,7 @@ def layer_step(w, layer):
     ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
     ops.paged_decode(
         w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
-        out=w.out[layer], workspace=w.workspace,
+        out=w.out[layer], workspace=w.workspace, shared_prefix=w.prefix_hint,
     )
 
 
@@ -348,7 +355,8 @@ def step_bytes(lengths, shared_tokens=0):
 
     Returns (loop-step bytes, decode-launch bytes, decode-launch unique bytes):
     the unique figure counts the K/V of `shared_tokens` aliased prefix tokens
-    once per launch instead of once per row that reads them.
+    once per launch instead of once per row that reads them, and so does the
+    loop-step figure (the decode reads the shared pages once per launch).
     """
     kv_token = 2 * HKV * HEAD_DIM * 2  # K+V of one token in one layer (8 KiB)
     qo = 2 * HQ * HEAD_DIM * 2  # q read + out write
@@ -356,7 +364,7 @@ def step_bytes(lengths, shared_tokens=0):
     decode = sum(kv_token * n + qo + 4 * math.ceil(n / PAGE) + 4 for n in lengths)
     append = len(lengths) * (2 * new_kv + 16)  # read new k/v, write the page slots, block+offset
     unique = decode - kv_token * shared_tokens * (len(lengths) - 1) if shared_tokens else decode
-    return LAYERS * (decode + append), decode, unique
+    return LAYERS * (unique + append), decode, unique
 
 
 def spot_check(w):
@@ -767,7 +775,7 @@ def main():
             start.record(stream)
             ops.paged_decode(
                 w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
-                out=w.out[layer], workspace=w.workspace,
+                out=w.out[layer], workspace=w.workspace, shared_prefix=w.prefix_hint,
             )
             end.record(stream)
             pairs.append((start, end))
@@ -812,7 +820,10 @@ def main():
         "step_ms_median": round(statistics.median(step_ms), 4),
         "step_ms_iqr": iqr(step_ms),
         "roofline": {
-            "kernel": "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)",
+            "kernel": "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
+            if w.prefix_hint is None
+            else "rlt_paged_decode_shared_prefix (shared_prefix_kernel + paged_decode_kernel split pass + "
+            "paged_decode_merge_kernel)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

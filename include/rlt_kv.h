@@ -193,6 +193,37 @@ int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_ca
                      int64_t workspace_bytes, void* stream);
 
 /*
+ * rlt_paged_decode for a batch whose listed rows alias one prefix (prefix-cache
+ * pages shared read-only, vllm_rlt/core/kv_cache_manager.py:240-293).  Same
+ * contract and result as rlt_paged_decode, which it replaces for such a batch;
+ * the reference reads the shared pages once per row, this reads them once per
+ * launch.
+ *   prefix_member: device int32 [n_rows], nonzero for rows whose first
+ *     prefix_pages table entries are prefix_table (device int32
+ *     [prefix_pages]).  prefix_rows: device int32 [n_prefix_rows], exactly
+ *     those rows, any order.
+ *   prefix_split_len: 256 << k; the prefix pass serves the split-K splits of
+ *     member rows whose split length (a function of their length alone) it is.
+ * The shared splits of member rows are computed once for all of them (bf16 or
+ * fp16, head_dim 128, q heads per KV head 1/2/4/8, page 16) and merged with
+ * each row's remaining splits.  A split is taken from the prefix pass only if
+ * the row's table entries for it equal prefix_table's, so an inexact hint
+ * costs speed, not correctness; other shapes ignore the hint.  Rows must not be
+ * more than 8192.
+ */
+int rlt_paged_decode_shared_prefix(const void* q, const int64_t* q_strides, const void* key_cache,
+                                   const void* value_cache, const int64_t* kv_strides,
+                                   const int32_t* block_tables, int64_t table_stride,
+                                   int64_t max_table_width, const int32_t* context_lengths,
+                                   void* out, const int64_t* out_strides, int64_t n_rows,
+                                   int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                   int64_t page_size, int64_t num_blocks, float scale, int dtype,
+                                   void* workspace, int64_t workspace_bytes,
+                                   const int32_t* prefix_member, const int32_t* prefix_rows,
+                                   int64_t n_prefix_rows, const int32_t* prefix_table,
+                                   int64_t prefix_pages, int64_t prefix_split_len, void* stream);
+
+/*
  * Workspace bytes rlt_paged_prefill needs (shape-only, no sync needed).  Zero
  * for the MFMA path (bf16/fp16, head_dim 64 or 128, page 16, 16-byte aligned
  * rows); otherwise the size of the per-token decode-row path.

@@ -35,8 +35,10 @@
 // agent-scope release/acquire per split -- an L2 writeback and invalidate
 // across the 8 XCDs -- and measured 3x slower than the separate merge.)
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
+#include "mfma.hpp"
 
 namespace rlt {
 namespace {
@@ -106,12 +108,38 @@ struct DecodeArgs {
   int64_t num_blocks;
   int64_t max_len;  // table width * page: lengths are clamped to what the table covers
   float qscale;     // softmax scale * log2(e)
+  // Shared prefix (all null / 0 when absent): rows with prefix_member[r] != 0
+  // begin with the prefix_pages pages of prefix_table; prefix_rows lists
+  // exactly those rows.  Their splits inside the prefix (at split length
+  // prefix_split_len) come from shared_prefix_kernel instead of the split pass.
+  const int32_t* prefix_member;
+  const int32_t* prefix_rows;
+  const int32_t* prefix_table;
+  int n_prefix_rows, prefix_pages, prefix_split_len;
 };
 
 // A row's effective context length; never reaches past its table row.
 __device__ __forceinline__ int row_length(const DecodeArgs& a, int r) {
   const int64_t len = a.lens[r];
   return static_cast<int>(len < a.max_len ? len : a.max_len);
+}
+
+// True when split sp of row r (split_len tokens, ns splits) is computed by
+// shared_prefix_kernel rather than by the split pass.  Both kernels evaluate
+// this same predicate, so every split is produced exactly once.  The split
+// must lie inside the shared prefix, leave at least one split of the row to
+// the split pass (so the row goes through the merge), use the prefix pass's
+// split length, and read exactly the shared pages.
+__device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
+  if (!a.prefix_member || !a.prefix_member[r] || split_len != a.prefix_split_len) return false;
+  const int64_t covered = static_cast<int64_t>(a.prefix_pages) * a.page / split_len;
+  if (sp >= covered || sp >= ns - 1) return false;
+  const int pages = split_len / a.page;
+  const int32_t* trow = a.tables + static_cast<int64_t>(r) * a.table_stride + sp * pages;
+  const int32_t* shared = a.prefix_table + sp * pages;
+  bool same = true;
+  for (int i = 0; i < pages; ++i) same &= trow[i] == shared[i];
+  return same;
 }
 
 // K/V page reads: each byte is read once per launch.
@@ -228,7 +256,7 @@ __device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int la
   }
 }
 
-template <typename T, int D, int G, int P, int TILE, bool XCD>
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   using PK = Packet<T>;
   constexpr int EPL = PK::N;      // elements of one token a lane owns
@@ -459,7 +487,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int len = uniform(row_length(a, r));
     int split_len, ns;
     split_plan(len, &split_len, &ns);
-    if (sp < ns) process(r, h, sp, len, split_len, ns);
+    if (sp < ns && !(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
   } else {
     // Packed schedule (any head count): the compact list of rows x splits x
     // kv heads, kv head innermost, walked in grid-stride order.
@@ -474,7 +502,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       const int len = uniform(row_length(a, r));
       int split_len, ns;
       split_plan(len, &split_len, &ns);
-      process(r, h, sp, len, split_len, ns);
+      if (!(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
     }
   }
 }
@@ -489,6 +517,172 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   int split_len, ns;
   split_plan(row_length(a, r), &split_len, &ns);
   if (ns > 1) merge_partials<T, D>(a, r, h, ns, threadIdx.x & 63);
+}
+
+// Shared-prefix pass: the split partials of the splits that prefix_takes()
+// gives it, for every listed row at once.  Workgroup (sp, h, b) owns split sp
+// of the shared prefix (keys [sp * S, (sp + 1) * S) of prefix_table, S =
+// prefix_split_len) under kv head h, for 64 queries: (row, q head) pairs
+// b * 64 .. b * 64 + 63 of prefix_rows x G, 32 per wave.  K and V of each
+// 32-key tile are read once into LDS (row-major, padded rows) and serve all 64
+// queries, so the prefix is read from memory once per launch instead of once
+// per row.  Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32
+// K rows, B = its 32 queries' q), keeps an online softmax in log2 units (the
+// running maximum moves only when a tile exceeds it by 2^kRescale), and
+// accumulates O^T += V^T P^T with P rounded to T and V^T from transposing LDS
+// reads; the row sums come from the same rounded P through one MFMA against
+// ones.  The result is written as the split pass would: (max, sum) and the
+// unnormalised accumulator in the decode workspace slot of (row, h, sp).
+constexpr int kPrefixBK = 32;   // keys per tile
+constexpr float kPrefixRescale = 8.f;
+
+template <typename T, int G>
+__global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
+  using Ops = MfmaOps<T>;
+  using V8 = typename Ops::V8;
+  constexpr int D = 128, KSTEPS = D / 16, DTILES = D / 32;
+  constexpr int KROW = D + 8, VROW = D + 32;  // padded rows: conflict-light K and transposing V reads
+  __shared__ __align__(16) uint16_t k_lds[kPrefixBK * KROW];
+  __shared__ __align__(16) uint16_t v_lds[kPrefixBK * VROW];
+
+  const int sp = blockIdx.x;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+
+  // This lane's query: (prefix_rows[qi / G], q head h * G + qi % G).
+  const int qi = blockIdx.z * 64 + wave * 32 + col;
+  const bool listed = qi < a.n_prefix_rows * G;
+  const int r = a.prefix_rows[listed ? qi / G : 0];
+  const int j = listed ? qi % G : 0;
+  bool mine = false;
+  if (listed && r >= 0 && r < a.n_rows) {
+    int split_len, ns;
+    split_plan(row_length(a, r), &split_len, &ns);
+    mine = prefix_takes(a, r, sp, split_len, ns);
+  }
+  if (!__syncthreads_or(mine)) return;
+  const int rq = mine ? r : 0;
+
+  // q as the B operand: lane (col, half) holds dims 16ks + 8half .. + 7.
+  u32x4 qb[KSTEPS];
+  {
+    const T* qrow = static_cast<const T*>(a.q) + rq * a.q_row + static_cast<int64_t>(h * G + j) * a.q_head;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
+  }
+
+  // Staging: thread t moves 16-byte chunk (t + 128i) % 16 of tile row
+  // (t + 128i) / 16, i = 0..3, for K and for V.
+  const int S = a.prefix_split_len;
+  const int key0 = sp * S;
+  const int ntiles = S / kPrefixBK;
+  const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.kv_head;
+  const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.kv_head;
+  u32x4 kreg[4], vreg[4];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 128 * i;
+      const int key = key0 + t * kPrefixBK + (c >> 4);
+      const int64_t b = a.prefix_table[key / a.page];
+      const int64_t blk = (b < 0 || b >= a.num_blocks) ? 0 : b;
+      const int64_t off = blk * a.kv_block + static_cast<int64_t>(key % a.page) * a.kv_token + (c & 15) * 8;
+      kreg[i] = load_page(reinterpret_cast<const u32x4*>(kbase + off));
+      vreg[i] = load_page(reinterpret_cast<const u32x4*>(vbase + off));
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 128 * i;
+      *reinterpret_cast<u32x4*>(&k_lds[(c >> 4) * KROW + (c & 15) * 8]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&v_lds[(c >> 4) * VROW + (c & 15) * 8]) = vreg[i];
+    }
+  };
+
+  // V^T A-operand reads: within k-step ks, lane (dim i, half kh) needs keys
+  // 16ks + 4kh + {0..3} and 16ks + 8 + 4kh + {0..3}, the key order in which
+  // the S^T accumulator leaves P.
+  const int grp = lane >> 4, gl = lane & 15;
+  const int tr_off = (4 * (grp >> 1) + (gl >> 2)) * VROW + 16 * (grp & 1) + 4 * (gl & 3);
+  const uint32_t one2 = Ops::pack2(1.f, 1.f);
+  const u32x4 ones = {one2, one2, one2, one2};
+
+  f32x16 acc_o[DTILES];
+#pragma unroll
+  for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
+  f32x16 acc_l = f32x16{};
+  float m = -INFINITY;
+
+  load_tile(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();  // the previous tile's reads are done
+    store_tile();
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile(t + 1);
+    f32x16 sacc = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[col * KROW + ks * 16 + half * 8]);
+      sacc = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), sacc);
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sacc[e] *= a.qscale;
+      tmax = fmaxf(tmax, sacc[e]);
+    }
+    tmax = max_across_halves(tmax);
+    if (__builtin_amdgcn_ballot_w64(tmax > m + kPrefixRescale) != 0) {
+      const float mn = fmaxf(m, tmax);
+      const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+#pragma unroll
+      for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[c][e] *= corr;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_l[e] *= corr;
+      m = mn;
+    }
+    const float mb = (m == -INFINITY) ? 0.f : m;
+    u32x4 pb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pb[ks][e] = Ops::pack2(fast_exp2(sacc[ks * 8 + 2 * e] - mb), fast_exp2(sacc[ks * 8 + 2 * e + 1] - mb));
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int c = 0; c < DTILES; ++c) {
+        const uint16_t* vlo = &v_lds[tr_off + ks * 16 * VROW + c * 32];
+        const u32x2 lo = lds_read_tr(vlo);
+        const u32x2 hi = lds_read_tr(vlo + 8 * VROW);
+        const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
+        acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb[ks]), acc_o[c]);
+      }
+      acc_l = Ops::mma(as_v8<V8>(ones), as_v8<V8>(pb[ks]), acc_l);
+    }
+  }
+
+  if (!mine) return;
+  // O^T element e of dim tile c is dim 32c + 8(e/4) + 4half + e%4.
+  const int64_t slot = (static_cast<int64_t>(rq) * a.hkv + h) * kMaxSplits + sp;
+  float* dst = a.ws_acc + (slot * G + j) * D + 4 * half;
+#pragma unroll
+  for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(acc_o[c][4 * g4 + e]);
+      *reinterpret_cast<u32x4*>(dst + 32 * c + 8 * g4) = w;
+    }
+  if (half == 0) a.ws_ml[slot * G + j] = make_float2(m, acc_l[0]);
 }
 
 // Generic kernel for shapes the tiled kernel does not cover (odd head_dim,
@@ -557,52 +751,87 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
 // Host dispatch.
 using DecodeKernel = void (*)(DecodeArgs);
 
-template <typename T, int D, bool XCD>
+template <typename T, int D, bool XCD, bool PREFIX>
 DecodeKernel pick_group(int G) {
   switch (G) {
-    case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD>;
-    case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD>;
-    case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD>;
-    case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD>;
+    case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, PREFIX>;
+    case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, PREFIX>;
+    case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, PREFIX>;
+    case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, PREFIX>;
     default: return nullptr;
   }
 }
 
+// The split pass with the shared-prefix check exists where the prefix pass
+// does (16-bit types, head_dim 128); everywhere else it is compiled out.
 template <typename T, int D>
-DecodeKernel pick_group(int G, bool xcd) {
-  return xcd ? pick_group<T, D, true>(G) : pick_group<T, D, false>(G);
+DecodeKernel pick_group(int G, bool xcd, bool prefix) {
+  if (prefix) {
+    if constexpr (D == 128 && !std::is_same_v<T, float>)
+      return xcd ? pick_group<T, D, true, true>(G) : pick_group<T, D, false, true>(G);
+    return nullptr;
+  }
+  return xcd ? pick_group<T, D, true, false>(G) : pick_group<T, D, false, false>(G);
 }
 
 template <typename T>
-DecodeKernel pick_tiled(int d, int G, bool xcd);
+DecodeKernel pick_tiled(int d, int G, bool xcd, bool prefix);
 template <>
-DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd) {
+DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd, bool prefix) {
   switch (d) {
-    case 64: return pick_group<bf16, 64>(G, xcd);
-    case 128: return pick_group<bf16, 128>(G, xcd);
-    case 256: return pick_group<bf16, 256>(G, xcd);
+    case 64: return pick_group<bf16, 64>(G, xcd, prefix);
+    case 128: return pick_group<bf16, 128>(G, xcd, prefix);
+    case 256: return pick_group<bf16, 256>(G, xcd, prefix);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<f16>(int d, int G, bool xcd) {
+DecodeKernel pick_tiled<f16>(int d, int G, bool xcd, bool prefix) {
   switch (d) {
-    case 64: return pick_group<f16, 64>(G, xcd);
-    case 128: return pick_group<f16, 128>(G, xcd);
-    case 256: return pick_group<f16, 256>(G, xcd);
+    case 64: return pick_group<f16, 64>(G, xcd, prefix);
+    case 128: return pick_group<f16, 128>(G, xcd, prefix);
+    case 256: return pick_group<f16, 256>(G, xcd, prefix);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<float>(int d, int G, bool xcd) {
+DecodeKernel pick_tiled<float>(int d, int G, bool xcd, bool prefix) {
   switch (d) {
-    case 64: return pick_group<float, 64>(G, xcd);
-    case 128: return pick_group<float, 128>(G, xcd);
+    case 64: return pick_group<float, 64>(G, xcd, prefix);
+    case 128: return pick_group<float, 128>(G, xcd, prefix);
     default: return nullptr;
   }
 }
 
 bool stride16(int64_t stride, int esize) { return (stride * esize) % 16 == 0; }
+
+// Launches the shared-prefix pass; false when it does not exist for this
+// shape (the caller then drops the hint and the split pass computes every
+// split itself).
+template <typename T>
+bool launch_shared_prefix(const DecodeArgs& a, hipStream_t stream) {
+  if constexpr (std::is_same_v<T, float>) {
+    return false;
+  } else {
+    if (a.d != 128) return false;
+    void (*kernel)(DecodeArgs) = nullptr;
+    switch (a.hq / a.hkv) {
+      case 1: kernel = shared_prefix_kernel<T, 1>; break;
+      case 2: kernel = shared_prefix_kernel<T, 2>; break;
+      case 4: kernel = shared_prefix_kernel<T, 4>; break;
+      case 8: kernel = shared_prefix_kernel<T, 8>; break;
+      default: return false;
+    }
+    const int64_t splits = std::min<int64_t>(static_cast<int64_t>(a.prefix_pages) * a.page / a.prefix_split_len,
+                                             kMaxSplits - 1);
+    if (splits <= 0) return false;
+    const int64_t queries = static_cast<int64_t>(a.n_prefix_rows) * (a.hq / a.hkv);
+    const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a.hkv),
+                    static_cast<unsigned>((queries + 63) / 64));
+    hipLaunchKernelGGL(kernel, grid, dim3(128), 0, stream, a);
+    return true;
+  }
+}
 
 template <typename T>
 int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
@@ -615,7 +844,12 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
                          stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
                          a.kv_token * a.page < (int64_t(1) << 31);
   const bool xcd = RLT_DECODE_XCD_SCHEDULE && a.hkv % kWaves == 0;
-  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd);
+  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, false);
+  if (a.prefix_member && !(tiled && launch_shared_prefix<T>(a, stream))) a.prefix_member = nullptr;
+  if (a.prefix_member) {
+    if (int rc = check_launch("rlt_paged_decode_shared_prefix(prefix)")) return rc;
+    tiled = pick_tiled<T>(a.d, G, xcd, true);
+  }
   if (!tiled) {
     if (a.d > 64 * kGenericMaxPerLane) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: head_dim > 512");
     if (a.hq > 65535) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: too many query heads");
@@ -677,12 +911,22 @@ extern "C" int64_t rlt_paged_decode_workspace_bytes(int64_t n_rows, int64_t num_
   return workspace_bytes_for(n_rows, num_q_heads, num_kv_heads, head_dim);
 }
 
-extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
-                                const void* value_cache, const int64_t* kv_strides, const int32_t* block_tables,
-                                int64_t table_stride, int64_t max_table_width, const int32_t* context_lengths,
-                                void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
-                                int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks,
-                                float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+struct PrefixHint {
+  const int32_t* member;
+  const int32_t* rows;
+  int64_t n_rows;
+  const int32_t* table;
+  int64_t pages, split_len;
+};
+
+int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache, const void* value_cache,
+                 const int64_t* kv_strides, const int32_t* block_tables, int64_t table_stride, int64_t max_table_width,
+                 const int32_t* context_lengths, void* out, const int64_t* out_strides, int64_t n_rows,
+                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks,
+                 float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream,
+                 const PrefixHint* hint) {
   const int esize = dtype_size(dtype);
   if (!esize) return fail(RLT_EINVAL, "rlt_paged_decode: unknown dtype %d", dtype);
   if (n_rows < 0) return fail(RLT_EINVAL, "rlt_paged_decode: n_rows is negative");
@@ -728,6 +972,14 @@ extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const v
   a.num_blocks = num_blocks;
   a.max_len = max_table_width * page_size;
   a.qscale = scale * kLog2e;
+  if (hint) {
+    a.prefix_member = hint->member;
+    a.prefix_rows = hint->rows;
+    a.n_prefix_rows = static_cast<int>(hint->n_rows);
+    a.prefix_table = hint->table;
+    a.prefix_pages = static_cast<int>(hint->pages);
+    a.prefix_split_len = static_cast<int>(hint->split_len);
+  }
   hipStream_t s = as_stream(stream);
   for (int64_t r0 = 0; r0 < n_rows; r0 += kMaxRowsPerLaunch) {
     const int64_t rows = std::min<int64_t>(kMaxRowsPerLaunch, n_rows - r0);
@@ -745,4 +997,43 @@ extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const v
     if (rc) return rc;
   }
   return RLT_OK;
+}
+
+}  // namespace
+
+extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
+                                const void* value_cache, const int64_t* kv_strides, const int32_t* block_tables,
+                                int64_t table_stride, int64_t max_table_width, const int32_t* context_lengths,
+                                void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
+                                int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks,
+                                float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  return paged_decode(q, q_strides, key_cache, value_cache, kv_strides, block_tables, table_stride, max_table_width,
+                      context_lengths, out, out_strides, n_rows, num_q_heads, num_kv_heads, head_dim, page_size,
+                      num_blocks, scale, dtype, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int rlt_paged_decode_shared_prefix(
+    const void* q, const int64_t* q_strides, const void* key_cache, const void* value_cache,
+    const int64_t* kv_strides, const int32_t* block_tables, int64_t table_stride, int64_t max_table_width,
+    const int32_t* context_lengths, void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks, float scale, int dtype,
+    void* workspace, int64_t workspace_bytes, const int32_t* prefix_member, const int32_t* prefix_rows,
+    int64_t n_prefix_rows, const int32_t* prefix_table, int64_t prefix_pages, int64_t prefix_split_len,
+    void* stream) {
+  if (!prefix_member || !prefix_rows || !prefix_table)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: NULL prefix argument");
+  if (n_prefix_rows < 1 || n_prefix_rows > n_rows)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_prefix_rows must be in [1, n_rows]");
+  if (n_rows > kMaxRowsPerLaunch)
+    return fail(RLT_EUNSUPPORTED, "rlt_paged_decode_shared_prefix: more than %d rows", kMaxRowsPerLaunch);
+  if (prefix_split_len < kSplitTokens || (prefix_split_len & (prefix_split_len - 1)) || page_size <= 0 ||
+      prefix_split_len % page_size)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: prefix_split_len must be %d << k and a page multiple",
+                kSplitTokens);
+  if (prefix_pages < 1 || prefix_pages > max_table_width)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: prefix_pages must be in [1, max_table_width]");
+  const PrefixHint hint{prefix_member, prefix_rows, n_prefix_rows, prefix_table, prefix_pages, prefix_split_len};
+  return paged_decode(q, q_strides, key_cache, value_cache, kv_strides, block_tables, table_stride, max_table_width,
+                      context_lengths, out, out_strides, n_rows, num_q_heads, num_kv_heads, head_dim, page_size,
+                      num_blocks, scale, dtype, workspace, workspace_bytes, stream, &hint);
 }

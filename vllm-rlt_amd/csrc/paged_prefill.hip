@@ -30,6 +30,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "mfma.hpp"
 
 namespace rlt {
 namespace {
@@ -67,17 +68,6 @@ __global__ __launch_bounds__(kThreads) void expand_rows_kernel(ExpandArgs a) {
 
 // ---------------------------------------------------------------------------
 // MFMA prefill kernel.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-typedef __attribute__((address_space(3))) uint16_t lds_u16;
-typedef __attribute__((address_space(3))) uint32_t lds_u32;
-typedef __attribute__((address_space(1))) void global_void;
 
 // Direct global->LDS loads.  They are written as assembly so that the
 // compiler's wait analysis, which cannot tell the tile buffers apart, does not
@@ -122,17 +112,6 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-// max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges one
-// register's upper 32 lanes with another's lower 32, so two copies of x end
-// up holding the two halves' values in swapped order, whichever way round.
-// The waits cover the VALU->permlane and permlane->VALU hazards, which the
-// compiler does not see inside assembly.
-__device__ __forceinline__ float max_across_halves(float x) {
-  float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-  return fmaxf(a, b);
-}
-
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kPage = 16;
@@ -171,39 +150,6 @@ struct PrefillArgs {
 __device__ __forceinline__ void seq_rows(const PrefillArgs& a, int s, int& row0, int& nq) {
   row0 = min(max(a.cu[s], 0), a.total_q);
   nq = min(max(a.cu[s + 1], row0), a.total_q) - row0;
-}
-
-template <typename T> struct MfmaOps;
-template <> struct MfmaOps<bf16> {
-  using V8 = bf16x8;
-  __device__ static f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
-  __device__ static uint32_t pack2(float x, float y) {
-    const bf16x2 r = {static_cast<__bf16>(x), static_cast<__bf16>(y)};  // v_cvt_pk_bf16_f32, RNE
-    return __builtin_bit_cast(uint32_t, r);
-  }
-};
-template <> struct MfmaOps<f16> {
-  using V8 = f16x8;
-  __device__ static f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
-  __device__ static uint32_t pack2(float x, float y) {
-    const f16x2 r = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
-    return __builtin_bit_cast(uint32_t, r);
-  }
-};
-
-template <typename V8>
-__device__ __forceinline__ V8 as_v8(u32x4 x) {
-  return __builtin_bit_cast(V8, x);
-}
-
-// Transposing LDS read (ds_read_b64_tr_b16).  In each 16-lane group, lane L
-// supplies the address of 4 consecutive 16-bit elements; lane j receives
-// element j%4 of the chunks supplied by lanes j/4, j/4+4, j/4+8, j/4+12.  With
-// lane L addressing row L/4, column 4(L%4) of a row-major tile, lane j gets
-// rows 0..3 of column j -- four consecutive keys of one V column.
-__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
-  const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  return __builtin_bit_cast(u32x2, x);
 }
 
 // Work list.  A work item is (sequence, query tile of kBM rows, query head).

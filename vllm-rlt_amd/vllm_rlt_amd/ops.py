@@ -9,6 +9,7 @@ the CPU and nothing falls back to another implementation.
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -224,6 +225,57 @@ def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, hea
     return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))
 
 
+# rlt_paged_decode's split plan: rows are cut into splits of 256 tokens, and
+# a row needing more than 64 splits doubles the split length until 64 cover it.
+DECODE_SPLIT_TOKENS = 256
+DECODE_MAX_SPLITS = 64
+
+
+def decode_split_len(length: int) -> int:
+    """Split length rlt_paged_decode uses for a row of `length` tokens."""
+    per = DECODE_SPLIT_TOKENS
+    while -(-int(length) // per) > DECODE_MAX_SPLITS:
+        per <<= 1
+    return per
+
+
+@dataclass(frozen=True)
+class SharedPrefix:
+    """Rows of a decode batch whose block tables begin with the same pages.
+
+    member: int32 [rows], 1 for those rows.  rows: int32 [n], the same rows.
+    table: int32 [pages], the shared page ids.  split_len: the decode split
+    length (decode_split_len) of the member rows the prefix pass serves.
+    """
+
+    member: torch.Tensor
+    rows: torch.Tensor
+    table: torch.Tensor
+    split_len: int
+
+
+def shared_prefix(rows, pages, n_rows: int, lengths, device) -> SharedPrefix:
+    """A SharedPrefix for `rows` (indices into the batch) sharing page ids `pages`.
+
+    `lengths` are the member rows' context lengths (host values) and pick the
+    split length most of them use; members with another split length read the
+    prefix in the split pass, as without the hint.
+    """
+    rows = [int(r) for r in rows]
+    if not rows or len(set(rows)) != len(rows) or min(rows) < 0 or max(rows) >= n_rows:
+        raise ValueError("shared-prefix rows must be distinct batch rows")
+    splits = [decode_split_len(n) for n in lengths]
+    split_len = max(set(splits), key=splits.count) if splits else DECODE_SPLIT_TOKENS
+    member = torch.zeros(n_rows, dtype=torch.int32)
+    member[rows] = 1
+    return SharedPrefix(
+        member=member.to(device),
+        rows=torch.tensor(rows, dtype=torch.int32).to(device),
+        table=torch.as_tensor(pages, dtype=torch.int32).to(device),
+        split_len=split_len,
+    )
+
+
 def paged_decode(
     q: torch.Tensor,
     key_cache: torch.Tensor,
@@ -233,11 +285,14 @@ def paged_decode(
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     scale: float | None = None,
+    shared_prefix: SharedPrefix | None = None,
 ) -> torch.Tensor:
     """Paged decode attention over layer-slice caches [blocks, page, kv_heads, head_dim].
 
     Same contract as torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36):
-    returns a new tensor like q unless out is given.
+    returns a new tensor like q unless out is given.  With `shared_prefix` the
+    listed rows' common prefix pages are read once for all of them
+    (rlt_paged_decode_shared_prefix); the result is the same attention.
     """
     device = _require_rocm(q, key_cache, value_cache, block_tables, context_lengths)
     if q.ndim != 3 or key_cache.ndim != 4:
@@ -269,6 +324,28 @@ def paged_decode(
     elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
         raise ValueError(f"workspace must hold {need} bytes on {device}")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
+    if shared_prefix is not None:
+        sp = shared_prefix
+        _require_rocm(sp.member, sp.rows, sp.table)
+        _require_int(sp.member, torch.int32, "shared_prefix.member")
+        _require_int(sp.rows, torch.int32, "shared_prefix.rows")
+        _require_int(sp.table, torch.int32, "shared_prefix.table")
+        if sp.member.shape != (rows,) or not sp.member.is_contiguous():
+            raise ValueError("shared_prefix.member must be contiguous int32 [rows]")
+        if not sp.rows.is_contiguous() or not sp.table.is_contiguous():
+            raise ValueError("shared_prefix rows and table must be contiguous")
+        if sp.table.numel() > block_tables.shape[1]:
+            raise ValueError("the shared prefix is wider than the block tables")
+        rc = _native.load().rlt_paged_decode_shared_prefix(
+            q.data_ptr(), int64_array(q.stride()), key_cache.data_ptr(), value_cache.data_ptr(),
+            int64_array(key_cache.stride()), block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+            context_lengths.data_ptr(), out.data_ptr(), int64_array(out.stride()), rows, hq, hkv, d, page, nb, scale,
+            dtype_code(q.dtype), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            sp.member.data_ptr(), sp.rows.data_ptr(), sp.rows.numel(), sp.table.data_ptr(), sp.table.numel(),
+            sp.split_len, stream_handle(device),
+        )
+        check(rc, "rlt_paged_decode_shared_prefix")
+        return out
     rc = _native.load().rlt_paged_decode(
         q.data_ptr(),
         int64_array(q.stride()),
