@@ -152,3 +152,50 @@ def test_shared_prefix_arguments_are_checked():
     short = ops.SharedPrefix(hint.member[:1], hint.rows, hint.table, 256)
     with pytest.raises(ValueError, match=r"member must be contiguous int32 \[rows\]"):
         ops.paged_decode(dev.q, dev.key_slice, dev.value_slice, dev.tables, dev.lengths, shared_prefix=short)
+
+
+@pytest.mark.parametrize("share", [False, True])
+def test_manager_shares_the_prefix_reads_of_aliasing_rows(share):
+    # Requests b, c, d reuse a's published 800-token prefix (50 pages per
+    # depth, tests/test_prefix_growth.py:47-64); a decode batch of all four
+    # at depth 1 then reads those pages once when share_prefix_reads is set.
+    from dataclasses import replace
+
+    from vllm_rlt_amd import KVCacheManager
+
+    cache = KVCacheManager(1, 2, 128, 1024, 16, 2, device="cuda", dtype=torch.bfloat16,
+                           enable_prefix_caching=True, share_prefix_reads=share)
+    torch.manual_seed(21)
+    prompt = list(range(1000, 1801))
+    assert cache.allocate("a", 1400)
+    for depth in range(2):
+        kv = torch.randn(800, 2, 128, device="cuda", dtype=torch.bfloat16)
+        cache.write(0, ["a"] * 800, [depth] * 800, list(range(800)), kv, -kv)
+    cache.publish_prefix("a", prompt, 800)
+    hit = cache.lookup_prefix(prompt)
+    assert len(hit) == 50
+    ends = {"a": 1100, "b": 1000, "c": 1290, "d": 900}
+    for rid in ("b", "c", "d"):
+        assert cache.allocate(rid, 1400, prefix=hit)
+    for rid, end in ends.items():
+        for depth in range(2):
+            n = end - 800
+            kv = torch.randn(n, 2, 128, device="cuda", dtype=torch.bfloat16)
+            cache.write(0, [rid] * n, [depth] * n, list(range(800, end)), kv, kv * 0.5)
+    ids = list(ends)
+    batch = cache._prepare_batch(ids, [1] * 4, [ends[r] - 1 for r in ids], for_write=False)
+    q = torch.randn(4, 4, 128, device="cuda", dtype=torch.bfloat16)
+    out = cache._attend_prepared(0, batch, q)
+    if not share:
+        assert batch.shared_prefix is None
+        return
+    hint = batch.shared_prefix
+    assert hint.rows.tolist() == [0, 1, 2, 3] and hint.member.tolist() == [1, 1, 1, 1]
+    assert hint.table.tolist() == list(cache.get_block_table("b", 1)[:50]) and hint.split_len == 256
+    plain = cache._attend_prepared(0, replace(batch, shared_prefix=None), q)
+    torch.testing.assert_close(out, plain, atol=2e-2, rtol=1e-2)
+    expected = paged_attention_cpu(
+        q.cpu(), cache.key_cache[:, 0].cpu(), cache.value_cache[:, 0].cpu(), batch.block_tables.cpu(),
+        batch.context_lengths.cpu(),
+    )
+    torch.testing.assert_close(out.cpu(), expected, atol=2e-2, rtol=1e-2)

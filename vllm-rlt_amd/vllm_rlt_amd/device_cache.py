@@ -29,5 +29,6 @@ class DeviceCache:
     def _attend_prepared(self, layer, batch, q):
         cache = self.cache
         return cache.attention(
-            q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths
+            q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths,
+            shared_prefix=batch.shared_prefix,
         )

@@ -51,6 +51,7 @@ class KVCacheManager(KVPageBook):
         enable_prefix_caching: bool = False,
         incremental_allocation: bool = False,
         watermark_ratio: float = 0.0,
+        share_prefix_reads: bool = False,
     ):
         super().__init__(
             num_layers,
@@ -73,6 +74,11 @@ class KVCacheManager(KVPageBook):
             raise ValueError("the hip attention backend requires a ROCm device")
         self.backend = backend
         self.dtype = dtype
+        # Decode batches whose rows alias prefix pages read them once per
+        # launch (rlt_paged_decode_shared_prefix).  Off by default: a row's
+        # output bits then depend on which rows share its batch (within the
+        # attention tolerance), where otherwise they depend on the row alone.
+        self.share_prefix_reads = bool(share_prefix_reads)
         self.attention = HipPagedAttention(device, dtype, self.head_dim, self.block_size)
         self.attention_info = self.attention.info
         shape = (self.num_blocks, self.num_layers, self.block_size, self.num_kv_heads, self.head_dim)
@@ -94,8 +100,12 @@ class KVCacheManager(KVPageBook):
         n = len(plan.positions)
         t, w = plan.tables.shape
         s = 0 if plan.cu_seqlens is None else len(plan.cu_seqlens)
+        found = None
+        if self.share_prefix_reads and plan.cu_seqlens is None:
+            found = ops.find_shared_prefix(plan.tables, plan.lengths, self.block_size)
+        hint32 = 0 if found is None else t + len(found[0]) + len(found[1])
         n64 = 3 * n
-        n32 = t * w + t + s
+        n32 = t * w + t + s + hint32
         bytes64 = 8 * n64
         total = bytes64 + (4 * n32 + 7) // 8 * 8
         host = torch.empty(max(total, 8), dtype=torch.uint8, pin_memory=True)
@@ -109,7 +119,14 @@ class KVCacheManager(KVPageBook):
             h32[: t * w] = plan.tables.reshape(-1)
             h32[t * w : t * w + t] = plan.lengths
             if s:
-                h32[t * w + t :] = plan.cu_seqlens
+                h32[t * w + t : t * w + t + s] = plan.cu_seqlens
+            if found is not None:
+                base = t * w + t + s
+                member = h32[base : base + t]
+                member[:] = 0
+                member[found[0]] = 1
+                h32[base + t : base + t + len(found[0])] = found[0]
+                h32[base + t + len(found[0]) : base + hint32] = found[1]
         dev = host.to(self.device, non_blocking=True)
         d64 = dev[:bytes64].view(torch.int64) if n64 else torch.empty(0, dtype=torch.int64, device=self.device)
         d32 = (
@@ -129,6 +146,18 @@ class KVCacheManager(KVPageBook):
             writable=plan.writable,
             cu_seqlens_q=d32[t * w + t : t * w + t + s] if s else None,
             max_seqlen_q=plan.max_seqlen_q,
+            shared_prefix=None if found is None else self._shared_prefix_views(d32, t * w + t + s, t, found),
+        )
+
+    @staticmethod
+    def _shared_prefix_views(d32, base, t, found):
+        rows, pages, split_len = found
+        m = len(rows)
+        return ops.SharedPrefix(
+            member=d32[base : base + t],
+            rows=d32[base + t : base + t + m],
+            table=d32[base + t + m : base + t + m + len(pages)],
+            split_len=split_len,
         )
 
     # ------------------------------------------------------------ tensors
@@ -227,6 +256,11 @@ class KVCacheManager(KVPageBook):
                 batch.context_lengths,
                 batch.cu_seqlens_q,
                 batch.max_seqlen_q,
+            )
+        if batch.shared_prefix is not None:
+            return self.attention(
+                q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths,
+                shared_prefix=batch.shared_prefix,
             )
         return self.attention(
             q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths

@@ -254,6 +254,44 @@ class SharedPrefix:
     split_len: int
 
 
+def find_shared_prefix(tables, lengths, page: int):
+    """(rows, pages, split_len) of rows whose block tables begin with the same pages, or None.
+
+    tables: int32 [rows, W] host array (-1 padded); lengths: the rows' context
+    lengths.  Candidates are the live rows sharing the most common first page.
+    Each has a common prefix with the first of them (up to the first differing
+    or negative entry); of the prefix lengths that cover whole splits, the one
+    that saves the most split reads ((members - 1) x whole splits) wins, with
+    the rows whose common prefix reaches it.  None when that saves nothing.
+    """
+    import numpy as np
+
+    tables = np.asarray(tables)
+    lengths = np.asarray(lengths)
+    if tables.ndim != 2 or len(tables) < 2 or tables.shape[1] == 0:
+        return None
+    first = tables[:, 0]
+    valid = (first >= 0) & (lengths > 0)
+    values, counts = np.unique(first[valid], return_counts=True)
+    if not len(counts) or counts.max() < 2:
+        return None
+    rows = np.nonzero(valid & (first == values[counts.argmax()]))[0]
+    group = tables[rows]
+    eq = (group == group[0]) & (group[0] >= 0)
+    common = np.where(eq.all(axis=1), eq.shape[1], np.argmin(eq, axis=1))
+    splits = [decode_split_len(n) for n in lengths[rows]]
+    split_len = max(set(splits), key=splits.count)
+    best, best_gain = None, 0
+    for shared in sorted(set(common.tolist())):
+        members = int((common >= shared).sum())
+        gain = (members - 1) * (shared * page // split_len)
+        if gain > best_gain:
+            best, best_gain = shared, gain
+    if best is None:
+        return None
+    return rows[common >= best].tolist(), group[0, :best].tolist(), split_len
+
+
 def shared_prefix(rows, pages, n_rows: int, lengths, device) -> SharedPrefix:
     """A SharedPrefix for `rows` (indices into the batch) sharing page ids `pages`.
 

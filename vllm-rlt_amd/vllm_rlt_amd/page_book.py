@@ -90,6 +90,9 @@ class PreparedKVBatch:
     writable: bool
     cu_seqlens_q: torch.Tensor | None = None
     max_seqlen_q: int = 1
+    # Rows reading the same prefix pages, when the manager shares those reads
+    # (an ops.SharedPrefix; no counterpart in the reference's batch).
+    shared_prefix: Any = None
 
 
 @dataclass

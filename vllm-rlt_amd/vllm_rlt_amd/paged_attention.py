@@ -55,8 +55,10 @@ class HipPagedAttention:
             version=lib.rlt_version().decode(),
         )
 
-    def __call__(self, q, key_cache, value_cache, block_tables, context_lengths):
-        return ops.paged_decode(q, key_cache, value_cache, block_tables, context_lengths)
+    def __call__(self, q, key_cache, value_cache, block_tables, context_lengths, shared_prefix=None):
+        """Decode attention; `shared_prefix` (an ops.SharedPrefix, beyond the
+        reference's signature) reads rows' aliased prefix pages once."""
+        return ops.paged_decode(q, key_cache, value_cache, block_tables, context_lengths, shared_prefix=shared_prefix)
 
     def prefill(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q, max_seqlen_q):
         """Packed ragged chunks over paged prefixes, bottom-right causal.
