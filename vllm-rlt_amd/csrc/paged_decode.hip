@@ -582,8 +582,9 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
   const int ntiles = S / kPrefixBK;
   const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.kv_head;
   const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.kv_head;
-  u32x4 kreg[4], vreg[4];
-  auto load_tile = [&](int t) {
+  // Two tiles of loads in flight: tile t's registers are slot t % 2.
+  u32x4 kreg[2][4], vreg[2][4];
+  auto load_tile = [&](int t, u32x4 (&kr)[4], u32x4 (&vr)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 128 * i;
@@ -591,16 +592,16 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
       const int64_t b = a.prefix_table[key / a.page];
       const int64_t blk = (b < 0 || b >= a.num_blocks) ? 0 : b;
       const int64_t off = blk * a.kv_block + static_cast<int64_t>(key % a.page) * a.kv_token + (c & 15) * 8;
-      kreg[i] = load_page(reinterpret_cast<const u32x4*>(kbase + off));
-      vreg[i] = load_page(reinterpret_cast<const u32x4*>(vbase + off));
+      kr[i] = load_page(reinterpret_cast<const u32x4*>(kbase + off));
+      vr[i] = load_page(reinterpret_cast<const u32x4*>(vbase + off));
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](const u32x4 (&kr)[4], const u32x4 (&vr)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 128 * i;
-      *reinterpret_cast<u32x4*>(&k_lds[(c >> 4) * KROW + (c & 15) * 8]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&v_lds[(c >> 4) * VROW + (c & 15) * 8]) = vreg[i];
+      *reinterpret_cast<u32x4*>(&k_lds[(c >> 4) * KROW + (c & 15) * 8]) = kr[i];
+      *reinterpret_cast<u32x4*>(&v_lds[(c >> 4) * VROW + (c & 15) * 8]) = vr[i];
     }
   };
 
@@ -618,12 +619,7 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
   f32x16 acc_l = f32x16{};
   float m = -INFINITY;
 
-  load_tile(0);
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();  // the previous tile's reads are done
-    store_tile();
-    __syncthreads();
-    if (t + 1 < ntiles) load_tile(t + 1);
+  auto compute_tile = [&]() __attribute__((always_inline)) {
     f32x16 sacc = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -666,6 +662,19 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
         acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb[ks]), acc_o[c]);
       }
       acc_l = Ops::mma(as_v8<V8>(ones), as_v8<V8>(pb[ks]), acc_l);
+    }
+  };
+  // S = 256 << k keys, so the tile count is even.
+  load_tile(0, kreg[0], vreg[0]);
+  load_tile(1, kreg[1], vreg[1]);
+  for (int t = 0; t < ntiles; t += 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      __syncthreads();  // the previous tile's reads are done
+      store_tile(kreg[u], vreg[u]);
+      __syncthreads();
+      if (t + u + 2 < ntiles) load_tile(t + u + 2, kreg[u], vreg[u]);
+      compute_tile();
     }
   }
 
