@@ -229,6 +229,8 @@ def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, hea
 # a row needing more than 64 splits doubles the split length until 64 cover it.
 DECODE_SPLIT_TOKENS = 256
 DECODE_MAX_SPLITS = 64
+# rlt_paged_decode_shared_prefix serves batches of at most this many rows.
+DECODE_SHARED_PREFIX_MAX_ROWS = 8192
 
 
 def decode_split_len(length: int) -> int:
@@ -362,6 +364,8 @@ def paged_decode(
     elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
         raise ValueError(f"workspace must hold {need} bytes on {device}")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
+    if shared_prefix is not None and rows > DECODE_SHARED_PREFIX_MAX_ROWS:
+        shared_prefix = None  # an optimisation only: larger batches read the prefix per row
     if shared_prefix is not None:
         sp = shared_prefix
         _require_rocm(sp.member, sp.rows, sp.table)
