@@ -623,13 +623,16 @@ def run_prefill(args, device):
         w.step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    pairs = []
+    # Events are created before the pass, so no event creation sits between launches.
+    pairs = [
+        (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        for _ in range(args.steps * LOOPS * LAYERS)
+    ]
+    events = iter(pairs)
     for _ in range(args.steps):
         for depth in range(LOOPS):
             for layer in range(LAYERS):
-                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                w.layer(depth, layer, ev)
-                pairs.append(ev)
+                w.layer(depth, layer, next(events))
     torch.cuda.synchronize()
     launch_list = [a.elapsed_time(b) for a, b in pairs]
     launch_ms = statistics.fmean(launch_list)
@@ -766,19 +769,23 @@ def main():
     from vllm_rlt_amd import ops
 
     stream = torch.cuda.current_stream(device)
-    pairs = []
+    # Events are created before the pass, so no event creation sits between launches.
+    pairs = [
+        (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        for _ in range((total - args.warmup) * LAYERS)
+    ]
+    events = iter(pairs)
     for step in range(args.warmup, total):
         build_metadata(w, step)
         for layer in range(LAYERS):
             ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start, end = next(events)
             start.record(stream)
             ops.paged_decode(
                 w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
                 out=w.out[layer], workspace=w.workspace, shared_prefix=w.prefix_hint,
             )
             end.record(stream)
-            pairs.append((start, end))
     torch.cuda.synchronize()
     launch_ms = [s.elapsed_time(e) for s, e in pairs]
     decode_ms = statistics.fmean(launch_ms)
