@@ -11,6 +11,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _native
@@ -266,8 +267,6 @@ def find_shared_prefix(tables, lengths, page: int):
     that saves the most split reads ((members - 1) x whole splits) wins, with
     the rows whose common prefix reaches it.  None when that saves nothing.
     """
-    import numpy as np
-
     tables = np.asarray(tables)
     lengths = np.asarray(lengths)
     if tables.ndim != 2 or len(tables) < 2 or tables.shape[1] == 0:
