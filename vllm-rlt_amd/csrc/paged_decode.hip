@@ -523,10 +523,11 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 // gives it, for every listed row at once.  Workgroup (sp, h, b) owns split sp
 // of the shared prefix (keys [sp * S, (sp + 1) * S) of prefix_table, S =
 // prefix_split_len) under kv head h, for 64 queries: (row, q head) pairs
-// b * 64 .. b * 64 + 63 of prefix_rows x G, 32 per wave.  K and V of each
-// 32-key tile are read once into LDS (row-major, padded rows) and serve all 64
-// queries, so the prefix is read from memory once per launch instead of once
-// per row.  Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32
+// b * 64 .. b * 64 + 63 of prefix_rows x G.  Wave w takes queries 32(w % 2) ..
+// + 31 over key half w / 2 of the split; the two halves merge their (max, sum,
+// acc) through LDS at the end.  K and V of each 32-key tile are read once into
+// LDS (row-major, padded rows) and serve all 64 queries, so the prefix is read
+// from memory once per launch instead of once per row.  Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32
 // K rows, B = its 32 queries' q), keeps an online softmax in log2 units (the
 // running maximum moves only when a tile exceeds it by 2^kRescale), and
 // accumulates O^T += V^T P^T with P rounded to T and V^T from transposing LDS
@@ -537,24 +538,30 @@ constexpr int kPrefixBK = 32;   // keys per tile
 constexpr float kPrefixRescale = 8.f;
 
 template <typename T, int G>
-__global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   constexpr int D = 128, KSTEPS = D / 16, DTILES = D / 32;
   constexpr int KROW = D + 8, VROW = D + 32;  // padded rows: conflict-light K and transposing V reads
-  __shared__ __align__(16) uint16_t k_lds[kPrefixBK * KROW];
-  __shared__ __align__(16) uint16_t v_lds[kPrefixBK * VROW];
+  constexpr int KTILE = kPrefixBK * KROW, VTILE = kPrefixBK * VROW;
+  constexpr int MERGE_FLOATS = 2 + 16 * DTILES;  // (max, sum, acc) per lane
+  static_assert(2 * 64 * MERGE_FLOATS * 4 <= 2 * (KTILE + VTILE) * 2, "merge fits in the tile buffers");
+  __shared__ __align__(16) uint16_t tiles[2 * (KTILE + VTILE)];  // per key half: K tile, V tile
 
   const int sp = blockIdx.x;
   const int h = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
+  const int qw = wave & 1;   // query half
+  const int kh = wave >> 1;  // key half
   const int half = lane >> 5;
   const int col = lane & 31;
+  uint16_t* const k_lds = tiles + kh * (KTILE + VTILE);
+  uint16_t* const v_lds = k_lds + KTILE;
 
   // This lane's query: (prefix_rows[qi / G], q head h * G + qi % G).
-  const int qi = blockIdx.z * 64 + wave * 32 + col;
+  const int qi = blockIdx.z * 64 + qw * 32 + col;
   const bool listed = qi < a.n_prefix_rows * G;
   const int r = a.prefix_rows[listed ? qi / G : 0];
   const int j = listed ? qi % G : 0;
@@ -575,11 +582,12 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
     for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
   }
 
-  // Staging: thread t moves 16-byte chunk (t + 128i) % 16 of tile row
-  // (t + 128i) / 16, i = 0..3, for K and for V.
+  // Staging: within a key half, thread t (of 128) moves 16-byte chunk
+  // (t + 128i) % 16 of tile row (t + 128i) / 16, i = 0..3, for K and for V.
   const int S = a.prefix_split_len;
-  const int key0 = sp * S;
-  const int ntiles = S / kPrefixBK;
+  const int ntiles = S / kPrefixBK / 2;  // per key half
+  const int key0 = sp * S + kh * ntiles * kPrefixBK;
+  const int ltid = tid & 127;
   const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.kv_head;
   const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.kv_head;
   // Two tiles of loads in flight: tile t's registers are slot t % 2.
@@ -587,7 +595,7 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
   auto load_tile = [&](int t, u32x4 (&kr)[4], u32x4 (&vr)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + 128 * i;
+      const int c = ltid + 128 * i;
       const int key = key0 + t * kPrefixBK + (c >> 4);
       const int64_t b = a.prefix_table[key / a.page];
       const int64_t blk = (b < 0 || b >= a.num_blocks) ? 0 : b;
@@ -599,7 +607,7 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
   auto store_tile = [&](const u32x4 (&kr)[4], const u32x4 (&vr)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + 128 * i;
+      const int c = ltid + 128 * i;
       *reinterpret_cast<u32x4*>(&k_lds[(c >> 4) * KROW + (c & 15) * 8]) = kr[i];
       *reinterpret_cast<u32x4*>(&v_lds[(c >> 4) * VROW + (c & 15) * 8]) = vr[i];
     }
@@ -664,7 +672,7 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
       acc_l = Ops::mma(as_v8<V8>(ones), as_v8<V8>(pb[ks]), acc_l);
     }
   };
-  // S = 256 << k keys, so the tile count is even.
+  // S = 256 << k keys, so each key half has an even tile count.
   load_tile(0, kreg[0], vreg[0]);
   load_tile(1, kreg[1], vreg[1]);
   for (int t = 0; t < ntiles; t += 2) {
@@ -678,7 +686,29 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
     }
   }
 
-  if (!mine) return;
+  // Key half 1 hands its (max, sum, acc) to key half 0 through LDS.
+  __syncthreads();
+  float* xs = reinterpret_cast<float*>(tiles) + qw * MERGE_FLOATS * 64 + lane;
+  if (kh == 1) {
+    xs[0] = m;
+    xs[64] = acc_l[0];
+#pragma unroll
+    for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xs[(2 + 16 * c + e) * 64] = acc_o[c][e];
+  }
+  __syncthreads();
+  if (kh == 1 || !mine) return;
+  const float m1 = xs[0];
+  const float mm = fmaxf(m, m1);
+  const float c0 = (m == -INFINITY) ? 0.f : fast_exp2(m - mm);
+  const float c1 = (m1 == -INFINITY) ? 0.f : fast_exp2(m1 - mm);
+  const float l = acc_l[0] * c0 + xs[64] * c1;
+#pragma unroll
+  for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[c][e] = acc_o[c][e] * c0 + xs[(2 + 16 * c + e) * 64] * c1;
+  m = mm;
   // O^T element e of dim tile c is dim 32c + 8(e/4) + 4half + e%4.
   const int64_t slot = (static_cast<int64_t>(rq) * a.hkv + h) * kMaxSplits + sp;
   float* dst = a.ws_acc + (slot * G + j) * D + 4 * half;
@@ -691,7 +721,7 @@ __global__ __launch_bounds__(128) void shared_prefix_kernel(DecodeArgs a) {
       for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(acc_o[c][4 * g4 + e]);
       *reinterpret_cast<u32x4*>(dst + 32 * c + 8 * g4) = w;
     }
-  if (half == 0) a.ws_ml[slot * G + j] = make_float2(m, acc_l[0]);
+  if (half == 0) a.ws_ml[slot * G + j] = make_float2(m, l);
 }
 
 // Generic kernel for shapes the tiled kernel does not cover (odd head_dim,
@@ -837,7 +867,7 @@ bool launch_shared_prefix(const DecodeArgs& a, hipStream_t stream) {
     const int64_t queries = static_cast<int64_t>(a.n_prefix_rows) * (a.hq / a.hkv);
     const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a.hkv),
                     static_cast<unsigned>((queries + 63) / 64));
-    hipLaunchKernelGGL(kernel, grid, dim3(128), 0, stream, a);
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a);
     return true;
   }
 }
