@@ -199,3 +199,57 @@ def test_manager_shares_the_prefix_reads_of_aliasing_rows(share):
         batch.context_lengths.cpu(),
     )
     torch.testing.assert_close(out.cpu(), expected, atol=2e-2, rtol=1e-2)
+
+
+def test_shared_prefix_decode_replays_in_a_graph():
+    # A captured write+attend over rows that alias a published prefix (with
+    # the hint) replays to the eager result every time, eager work between.
+    from vllm_rlt_amd import DeviceCache, KVCacheManager
+
+    cache = KVCacheManager(2, 2, 128, 512, 16, 2, device="cuda", dtype=torch.bfloat16,
+                           enable_prefix_caching=True, share_prefix_reads=True)
+    torch.manual_seed(4)
+    prompt = list(range(2000, 2641))
+    assert cache.allocate("a", 1200)
+    for layer in range(2):
+        for depth in range(2):
+            kv = torch.randn(640, 2, 128, device="cuda", dtype=torch.bfloat16)
+            cache.write(layer, ["a"] * 640, [depth] * 640, list(range(640)), kv, -kv)
+    cache.publish_prefix("a", prompt, 640)
+    hit = cache.lookup_prefix(prompt)
+    ends = {"a": 1000, "b": 900, "c": 1100}
+    for rid in ("b", "c"):
+        assert cache.allocate(rid, 1200, prefix=hit)
+    for layer in range(2):
+        for rid, end in ends.items():
+            n = end - 640
+            kv = torch.randn(n, 2, 128, device="cuda", dtype=torch.bfloat16)
+            cache.write(layer, [rid] * n, [0] * n, list(range(640, end)), kv, kv)
+    ids = list(ends)
+    batch = cache._prepare_batch(ids, [0, 0, 0], [ends[r] for r in ids])
+    assert batch.shared_prefix is not None and batch.shared_prefix.rows.numel() == 3
+    k = torch.randn(3, 2, 128, device="cuda", dtype=torch.bfloat16)
+    q = torch.randn(3, 4, 128, device="cuda", dtype=torch.bfloat16)
+    proxy = DeviceCache(cache)
+
+    def core():
+        outs = []
+        for layer in range(2):
+            proxy._write_prepared(layer, batch, k + layer, k - layer)
+            outs.append(proxy._attend_prepared(layer, batch, q))
+        return torch.stack(outs)
+
+    eager = core().clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        core()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = core()
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(captured, eager, atol=0, rtol=0)
+        _ = (q * 2).sum().item()  # unrelated eager work between replays
