@@ -30,5 +30,5 @@ class DeviceCache:
         cache = self.cache
         return cache.attention(
             q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths,
-            shared_prefix=batch.shared_prefix,
+            shared_prefix=getattr(batch, "shared_prefix", None),
         )

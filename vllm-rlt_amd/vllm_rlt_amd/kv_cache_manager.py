@@ -257,10 +257,11 @@ class KVCacheManager(KVPageBook):
                 batch.cu_seqlens_q,
                 batch.max_seqlen_q,
             )
-        if batch.shared_prefix is not None:
+        shared_prefix = getattr(batch, "shared_prefix", None)  # absent from batches built by other code
+        if shared_prefix is not None:
             return self.attention(
                 q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths,
-                shared_prefix=batch.shared_prefix,
+                shared_prefix=shared_prefix,
             )
         return self.attention(
             q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths
