@@ -14,6 +14,7 @@ from .kv_cache_manager import KVCacheManager
 from .page_book import KVPageBook, PreparedKVBatch
 from .paged_attention import HipPagedAttention, hip_paged_attention
 from .prefill_metadata import PrefillMetadataBank
+from .prefill_order import PrefillItem, PrefillOrder
 
 __all__ = [
     "AsyncState",
@@ -21,7 +22,9 @@ __all__ = [
     "HipPagedAttention",
     "KVCacheManager",
     "KVPageBook",
+    "PrefillItem",
     "PrefillMetadataBank",
+    "PrefillOrder",
     "PreparedKVBatch",
     "RecurrentGraphs",
     "RoutingBank",
