@@ -18,6 +18,9 @@ Three fixtures pin what the reference's own tests leave open:
       ouro.py:39-70) and of the q/k rotation q * cos + _rotate_half(q) * sin
       (ouro.py:73-75, 108-109) in bf16 / fp16 / fp32.
 The fixture files hold data only (inputs and outputs).
+
+The reference tree is read-only: bytecode writing is switched off before the
+reference is put on sys.path, so importing it leaves no __pycache__ there.
 """
 
 import json
@@ -194,6 +197,7 @@ def rotary_cases():
 
 def main():
     reference = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    sys.dont_write_bytecode = True  # never write .pyc files into the reference tree
     sys.path.insert(0, reference)
     torch.set_num_threads(1)
     (OUT / "allocator_trace.json").write_text(json.dumps(allocator_trace(), indent=1))

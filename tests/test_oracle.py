@@ -263,14 +263,94 @@ def test_planted_attention_mistakes_are_caught(mistake):
     np.testing.assert_allclose(right.double().numpy(), f64, atol=2e-6, rtol=2e-5)
 
 
-def test_planted_copy_mistake_is_caught():
-    # Copying from the target plane instead of the exit plane breaks the exit-copy golden.
+def _exit_copy_golden(copy_token, finalize_batched):
+    """tests/test_kv_cache.py:38-59 run through both exit-copy restatements.
+
+    2 layers, 3 depths, page 2; the token at position 0 writes depths 0 and 1
+    with keys 10*layer + depth (values +100) and exits at depth 1.  Depth 2
+    must then equal depth 1 at every layer, depth 0 keeps its own values, and
+    the copies are physical: a later write at depth 1 leaves depth 2 at the
+    old value.  Returns the list of failed checks (empty when the golden holds).
+    """
     layers, page = 2, 2
-    key_pool = np.zeros((6, layers, page, 1, 4), dtype=np.float32)
-    key_pool[2:4] = 1.0
-    tables = np.array([[[0, 1], [2, 3], [4, 5]]], dtype=np.int32)
-    good = key_pool.copy()
-    kv_ops.finalize_batched([[0, 1, 0]], tables, good, good.copy(), max_loops=3, page=page)
-    bad = key_pool.copy()
-    bad[4, :, 0] = bad[0, :, 0]  # wrong source plane (0 instead of 1)
-    assert (good[4, :, 0] == 1.0).all() and not (bad[4, :, 0] == good[4, :, 0]).all()
+    tables = np.array([[[0, 1], [2, 3], [4, 5]]], dtype=np.int32)  # [slot, plane, page]
+    failed = []
+    for route in ("copy_token", "finalize_batched"):
+        # Distinct negative sentinels in every element, so any stray copy shows.
+        key_pool = -1.0 - np.arange(6 * layers * page * 4, dtype=np.float32).reshape(6, layers, page, 1, 4)
+        value_pool = key_pool - 1000.0
+        for layer in range(layers):
+            for depth in range(2):
+                keys = np.full((1, 1, 4), float(10 * layer + depth), dtype=np.float32)
+                kv_ops.append(key_pool, value_pool, layer, [tables[0, depth, 0]], [0], keys, keys + 100)
+        before_k, before_v = key_pool.copy(), value_pool.copy()
+        if route == "copy_token":
+            copy_token(key_pool, value_pool, int(tables[0, 1, 0]), [int(tables[0, 2, 0])], 0)
+        else:
+            finalize_batched([[0, 1, 0]], tables, key_pool, value_pool, max_loops=3, page=page)
+        for layer in range(layers):
+            read = {d: (kv_ops.gather(key_pool, layer, tables[0, d], 1, page),
+                        kv_ops.gather(value_pool, layer, tables[0, d], 1, page)) for d in range(3)}
+            if not ((read[0][0] == 10 * layer).all() and (read[0][1] == 10 * layer + 100).all()):
+                failed.append((route, layer, "depth 0 changed"))
+            if not ((read[2][0] == 10 * layer + 1).all() and (read[2][1] == 10 * layer + 101).all()):
+                failed.append((route, layer, "depth 2 is not depth 1"))
+        # Only the (page 4, offset 0) slot of every layer may change.
+        changed = (key_pool != before_k) | (value_pool != before_v)
+        changed[4, :, 0] = False
+        if changed.any():
+            failed.append((route, "a slot other than the target changed"))
+        # Physical copies: overwrite depth 1 at layer 0, depth 2 keeps the old keys (ones).
+        kv_ops.append(key_pool, value_pool, 0, [tables[0, 1, 0]], [0],
+                      np.zeros((1, 1, 4), np.float32), np.zeros((1, 1, 4), np.float32))
+        if not (kv_ops.gather(key_pool, 0, tables[0, 2], 1, page) == 1.0).all():
+            failed.append((route, "depth 2 aliases depth 1"))
+    return failed
+
+
+def test_exit_copy_restatements_pass_the_golden():
+    assert _exit_copy_golden(kv_ops.copy_token, kv_ops.finalize_batched) == []
+
+
+def _copy_token_mistake(mistake):
+    def copy_token(key_pool, value_pool, src_block, dst_blocks, offset):
+        for dst in dst_blocks:
+            if mistake == "reversed":
+                key_pool[src_block, :, offset] = key_pool[dst, :, offset]
+                value_pool[src_block, :, offset] = value_pool[dst, :, offset]
+            elif mistake == "first_layer_only":
+                key_pool[dst, 0, offset] = key_pool[src_block, 0, offset]
+                value_pool[dst, 0, offset] = value_pool[src_block, 0, offset]
+            elif mistake == "keys_into_values":
+                key_pool[dst, :, offset] = key_pool[src_block, :, offset]
+                value_pool[dst, :, offset] = key_pool[src_block, :, offset]
+            elif mistake == "whole_page":
+                key_pool[dst] = key_pool[src_block]
+                value_pool[dst] = value_pool[src_block]
+
+    return copy_token
+
+
+def _finalize_mistake(mistake):
+    def finalize_batched(descriptors, tables, key_pool, value_pool, max_loops, page):
+        for slot, depth, pos in np.asarray(descriptors).reshape(-1, 3):
+            # wrong_source: copy from plane 0 instead of the exit plane.
+            src = tables[slot, 0 if mistake == "wrong_source" else depth, pos // page]
+            first = depth if mistake == "includes_exit_plane" else depth + 1
+            for target in range(first, max_loops - (mistake == "stops_short")):
+                dst = tables[slot, target, pos // page]
+                key_pool[dst, :, pos % page] = key_pool[src, :, pos % page]
+                value_pool[dst, :, pos % page] = value_pool[src, :, pos % page]
+
+    return finalize_batched
+
+
+@pytest.mark.parametrize("mistake", ["reversed", "first_layer_only", "keys_into_values", "whole_page"])
+def test_planted_copy_token_mistakes_are_caught(mistake):
+    assert _exit_copy_golden(_copy_token_mistake(mistake), kv_ops.finalize_batched) != []
+
+
+@pytest.mark.parametrize("mistake", ["wrong_source", "stops_short"])
+def test_planted_finalize_mistakes_are_caught(mistake):
+    assert _exit_copy_golden(kv_ops.copy_token, _finalize_mistake(mistake)) != []
+    assert _exit_copy_golden(kv_ops.copy_token, _finalize_mistake(None)) == []
