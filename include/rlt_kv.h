@@ -193,6 +193,37 @@ int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_ca
                      int64_t workspace_bytes, void* stream);
 
 /*
+ * rlt_paged_decode without a workspace argument: allocates nothing.
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  Same arguments (minus the workspace), contract and
+ * output bits as rlt_paged_decode.
+ * The split-K partials live in a static 64 MiB device array of the library.
+ * Each device holds its own copy from the library's first use there until the
+ * process ends.  Its address is looked up once per device.  The stream must
+ * belong to the current device.
+ * Rows go through in chunks of rlt_paged_decode_no_alloc_rows_per_launch()
+ * rows (126 at 16 q heads x head_dim 128), one chunk after another on the
+ * stream.  A shape whose single row needs more than 64 MiB of partials is
+ * rejected with RLT_EUNSUPPORTED before anything is enqueued.
+ * Every call on one device shares the array: calls that overlap on one device
+ * (different streams, or several host threads) race and give wrong results.
+ * Nothing in the array has to start at zero.
+ */
+int rlt_paged_decode_no_alloc(const void* q, const int64_t* q_strides, const void* key_cache,
+                              const void* value_cache, const int64_t* kv_strides,
+                              const int32_t* block_tables, int64_t table_stride,
+                              int64_t max_table_width, const int32_t* context_lengths, void* out,
+                              const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
+                              int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                              int64_t num_blocks, float scale, int dtype, void* stream);
+
+/* Rows per launch of rlt_paged_decode_no_alloc for this head geometry (0 when
+ * even one row exceeds the static scratch or the heads are invalid). */
+int64_t rlt_paged_decode_no_alloc_rows_per_launch(int64_t num_q_heads, int64_t num_kv_heads,
+                                                  int64_t head_dim);
+
+/*
  * rlt_paged_decode for a batch whose listed rows alias one prefix (prefix-cache
  * pages shared read-only, vllm_rlt/core/kv_cache_manager.py:240-293).  Same
  * contract and result as rlt_paged_decode, which it replaces for such a batch;

@@ -35,10 +35,19 @@
 // agent-scope release/acquire per split -- an L2 writeback and invalidate
 // across the 8 XCDs -- and measured 3x slower than the separate merge.)
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
 #include "mfma.hpp"
+
+// Split-K partials of rlt_paged_decode_no_alloc: a fixed per-device array in
+// place of a caller workspace (64 MiB; see rlt_kv.h for the row chunking it
+// implies).  Host code never passes `scratch` itself to a kernel -- on the
+// host it is only a stand-in for the device symbol -- but the address
+// hipGetSymbolAddress returns for the current device.
+constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace rlt {
 namespace {
@@ -1049,6 +1058,96 @@ extern "C" int rlt_paged_decode(const void* q, const int64_t* q_strides, const v
   return paged_decode(q, q_strides, key_cache, value_cache, kv_strides, block_tables, table_stride, max_table_width,
                       context_lengths, out, out_strides, n_rows, num_q_heads, num_kv_heads, head_dim, page_size,
                       num_blocks, scale, dtype, workspace, workspace_bytes, stream, nullptr);
+}
+
+namespace rlt {
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per
+// device (each device holds its own copy of the array).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+int scratch_for_stream(void* stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(RLT_ELAUNCH, "rlt_paged_decode_no_alloc: no current HIP device");
+  if (stream) {
+    int stream_dev = -1;
+    if (hipStreamGetDevice(as_stream(stream), &stream_dev) != hipSuccess)
+      return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: invalid stream");
+    if (stream_dev != dev)
+      return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: the stream belongs to device %d, the current device is %d",
+                  stream_dev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(RLT_ELAUNCH, "rlt_paged_decode_no_alloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(err));
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return RLT_OK;
+}
+
+}  // namespace
+}  // namespace rlt
+
+extern "C" int64_t rlt_paged_decode_no_alloc_rows_per_launch(int64_t num_q_heads, int64_t num_kv_heads,
+                                                              int64_t head_dim) {
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_q_heads % num_kv_heads) return 0;
+  // Largest row count whose workspace layout fits the scratch array (at most
+  // one launch's worth of rows).
+  int64_t lo = 0, hi = kMaxRowsPerLaunch;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (workspace_bytes_for(mid, num_q_heads, num_kv_heads, head_dim) <= kNoAllocScratchBytes) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+extern "C" int rlt_paged_decode_no_alloc(const void* q, const int64_t* q_strides, const void* key_cache,
+                                         const void* value_cache, const int64_t* kv_strides,
+                                         const int32_t* block_tables, int64_t table_stride, int64_t max_table_width,
+                                         const int32_t* context_lengths, void* out, const int64_t* out_strides,
+                                         int64_t n_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                         int64_t page_size, int64_t num_blocks, float scale, int dtype,
+                                         void* stream) {
+  const int esize = dtype_size(dtype);
+  if (!esize) return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: unknown dtype %d", dtype);
+  if (n_rows < 0) return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: n_rows is negative");
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: query heads must be a positive multiple of KV heads");
+  if (head_dim <= 0) return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: head_dim must be positive");
+  if (n_rows == 0) return RLT_OK;
+  if (!q || !block_tables || !context_lengths || !out || !q_strides || !out_strides)
+    return fail(RLT_EINVAL, "rlt_paged_decode_no_alloc: NULL pointer argument");
+  const int64_t rows_per = rlt_paged_decode_no_alloc_rows_per_launch(num_q_heads, num_kv_heads, head_dim);
+  if (rows_per < 1)
+    return fail(RLT_EUNSUPPORTED,
+                "rlt_paged_decode_no_alloc: one row needs %lld bytes of split partials, more than the %lld-byte "
+                "static scratch; use rlt_paged_decode with a workspace",
+                (long long)workspace_bytes_for(1, num_q_heads, num_kv_heads, head_dim),
+                (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (int rc = scratch_for_stream(stream, &ws)) return rc;
+  // Row chunks run in stream order and reuse the scratch: each chunk's merge
+  // has finished before the next chunk's split pass overwrites the partials.
+  for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per) {
+    const int64_t rows = std::min<int64_t>(rows_per, n_rows - r0);
+    const int rc = paged_decode(static_cast<const char*>(q) + r0 * q_strides[0] * esize, q_strides, key_cache,
+                                value_cache, kv_strides, block_tables + r0 * table_stride, table_stride,
+                                max_table_width, context_lengths + r0, static_cast<char*>(out) + r0 * out_strides[0] * esize,
+                                out_strides, rows, num_q_heads, num_kv_heads, head_dim, page_size, num_blocks, scale,
+                                dtype, ws, kNoAllocScratchBytes, stream, nullptr);
+    if (rc) return rc;
+  }
+  return RLT_OK;
 }
 
 extern "C" int rlt_paged_decode_shared_prefix(
