@@ -223,7 +223,20 @@ def scatter_rows(values: torch.Tensor, slots: torch.Tensor, pool: torch.Tensor, 
 
 
 def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    """Bytes of split-K partials rlt_paged_decode needs for a batch of n_rows (shape only)."""
     return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))
+
+
+def prefill_workspace_bytes(
+    total_q: int, num_seqs: int, table_width: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+    page_size: int, dtype: torch.dtype,
+) -> int:
+    """Bytes rlt_paged_prefill needs (0 on the MFMA path: bf16/fp16, head_dim 64/128, page 16)."""
+    return int(
+        _native.load().rlt_paged_prefill_workspace_bytes(
+            total_q, num_seqs, table_width, num_q_heads, num_kv_heads, head_dim, page_size, dtype_code(dtype)
+        )
+    )
 
 
 # rlt_paged_decode's split plan: rows are cut into splits of 256 tokens, and
@@ -421,6 +434,11 @@ def _rows_aligned16(t: torch.Tensor) -> bool:
     return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((st * size) % 16 == 0 for st in t.stride()[:-1])
 
 
+def rows_aligned16(*tensors: torch.Tensor) -> bool:
+    """Whether every tensor's rows are 16-byte aligned (the prefill MFMA path's requirement)."""
+    return all(_rows_aligned16(t) for t in tensors)
+
+
 def paged_prefill(
     q: torch.Tensor,
     key_cache: torch.Tensor,
@@ -431,8 +449,15 @@ def paged_prefill(
     max_seqlen_q: int,
     out: torch.Tensor | None = None,
     scale: float | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Packed bottom-right-causal prefill (FlashPagedAttention.prefill, flash_attention.py:66-96)."""
+    """Packed bottom-right-causal prefill (FlashPagedAttention.prefill, flash_attention.py:66-96).
+
+    The MFMA path needs no workspace; other shapes (fp32, unaligned rows,
+    other head sizes) run each query row as a decode row and need
+    prefill_workspace_bytes(...) bytes, allocated here unless `workspace`
+    (a uint8 device tensor at least that large) is given.
+    """
     device = _require_rocm(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q)
     if q.ndim != 3 or key_cache.ndim != 4:
         raise ValueError("q must be [tokens, heads, head_dim] and caches [blocks, page, kv_heads, head_dim]")
@@ -463,7 +488,10 @@ def paged_prefill(
     if not all(_rows_aligned16(t) for t in (q, out, key_cache, value_cache)):
         code = _native.RLT_FLOAT32  # the MFMA path needs 16-byte rows; size the per-token fallback
     need = int(lib.rlt_paged_prefill_workspace_bytes(total, nseq, width, hq, hkv, d, page, code))
-    workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
+        raise ValueError(f"workspace must hold {need} bytes on {device}")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     rc = lib.rlt_paged_prefill(
         q.data_ptr(),
@@ -489,7 +517,7 @@ def paged_prefill(
         scale,
         dtype_code(q.dtype),
         workspace.data_ptr(),
-        need,
+        workspace.numel() * workspace.element_size(),
         stream_handle(device),
     )
     check(rc, "rlt_paged_prefill")

@@ -30,7 +30,16 @@ def hip_paged_attention(
 
 
 class HipPagedAttention:
-    """Attention backend object for KVCacheManager(backend="hip")."""
+    """Attention backend object for KVCacheManager(backend="hip").
+
+    The object owns one grow-only device workspace for the decode split
+    partials and the per-token prefill path, so steady-state calls allocate
+    nothing.  It grows to the next power of two when a batch needs more
+    (reserve() grows it ahead of a graph capture).  A buffer it outgrows is
+    kept alive, not freed, because a captured graph may still hold its
+    address.  Calls on one object are meant to run on one stream, in order:
+    two streams sharing the object at once would share the workspace.
+    """
 
     generation = None
     supports_packed_prefill = True
@@ -46,8 +55,11 @@ class HipPagedAttention:
         if block_size <= 0:
             raise ValueError("block_size must be positive")
         lib = _native.load()
+        self.device = device
         self.head_dim = head_dim
         self.block_size = block_size
+        self._workspace = None
+        self._outgrown = []
         self.info = dict(
             backend="hip",
             arch="gfx950",
@@ -55,10 +67,31 @@ class HipPagedAttention:
             version=lib.rlt_version().decode(),
         )
 
+    @property
+    def workspace_bytes(self) -> int:
+        return 0 if self._workspace is None else self._workspace.numel()
+
+    def reserve(self, nbytes: int) -> torch.Tensor:
+        """The workspace, grown to at least nbytes (a power of two, 1 MiB or more)."""
+        nbytes = int(nbytes)
+        if self._workspace is None or self._workspace.numel() < nbytes:
+            if self._workspace is not None:
+                self._outgrown.append(self._workspace)
+            size = 1 << max(20, (max(nbytes, 1) - 1).bit_length())
+            self._workspace = torch.empty(size, dtype=torch.uint8, device=self.device)
+        return self._workspace
+
+    def reserve_decode(self, rows: int, num_q_heads: int, num_kv_heads: int) -> torch.Tensor:
+        """Grow the workspace for decode batches of up to `rows` rows."""
+        return self.reserve(ops.decode_workspace_bytes(rows, num_q_heads, num_kv_heads, self.head_dim))
+
     def __call__(self, q, key_cache, value_cache, block_tables, context_lengths, shared_prefix=None):
         """Decode attention; `shared_prefix` (an ops.SharedPrefix, beyond the
         reference's signature) reads rows' aliased prefix pages once."""
-        return ops.paged_decode(q, key_cache, value_cache, block_tables, context_lengths, shared_prefix=shared_prefix)
+        workspace = self.reserve_decode(q.shape[0], q.shape[1], key_cache.shape[2]) if q.shape[0] else None
+        return ops.paged_decode(
+            q, key_cache, value_cache, block_tables, context_lengths, workspace=workspace, shared_prefix=shared_prefix
+        )
 
     def prefill(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q, max_seqlen_q):
         """Packed ragged chunks over paged prefixes, bottom-right causal.
@@ -67,4 +100,11 @@ class HipPagedAttention:
         end at its last query, so query i of an n_q-token chunk sees
         context_lengths[s] - (n_q - 1 - i) keys (flash_attention.py:76-80).
         """
-        return ops.paged_prefill(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q, max_seqlen_q)
+        need = ops.prefill_workspace_bytes(
+            q.shape[0], block_tables.shape[0], block_tables.shape[1], q.shape[1], key_cache.shape[2], self.head_dim,
+            self.block_size, q.dtype if ops.rows_aligned16(q, key_cache, value_cache) else torch.float32,
+        )
+        workspace = self.reserve(need) if need else None
+        return ops.paged_prefill(
+            q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q, max_seqlen_q, workspace=workspace
+        )
