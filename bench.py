@@ -334,18 +334,11 @@ def loop_step(w, step, descriptors=None):
 
 def capture_loop_step(w):
     """One loop-step captured in a HIP graph; its descriptors are read from a static buffer."""
+    from vllm_rlt_amd.graphs import GraphCache
+
     static = torch.empty_like(w.descriptors[0])
     static.copy_(w.descriptors[0])
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(2):
-            loop_step(w, 0, static)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        loop_step(w, 0, static)
+    graph, _ = GraphCache(w.device).capture("loop-step", lambda: loop_step(w, 0, static))
     torch.cuda.synchronize()
     return graph, static
 

@@ -121,6 +121,22 @@ int rlt_scatter_rows(const void* values, int64_t values_row_bytes_stride, const 
                      int64_t row_bytes, void* stream);
 
 /*
+ * Device-resident page tables updated in place from (index, value) pairs.
+ * Replaces the per-request table uploads of RoutingBank.transfer
+ * (vllm_rlt/worker/async_state.py:46-49: one pinned tensor and one copy
+ * `tables[slot, :, :width] = table` for every request whose table changed):
+ *   tables[patches[2i]] = (int32) patches[2i + 1]  for i < n
+ * over the flat int32 tables [slots, planes, width].  A caller ships only the
+ * entries the device does not hold yet (a new request's whole table, a
+ * growing request's new pages), all requests of a step in one launch.
+ * patches: int64 [n, 2], device or pinned host memory (read in place).
+ * Indices within one call must be distinct; one outside [0, table_elems) is
+ * skipped.
+ */
+int rlt_patch_tables(const int64_t* patches, int64_t n, int32_t* tables, int64_t table_elems,
+                     void* stream);
+
+/*
  * Whole-page export / import of the K and V pools (all layers of a page are one
  * contiguous block).  Replaces the page-by-page copies of preemption
  *   keys[row] = key_cache[block]   (vllm_rlt/engine/preemption.py:85-89)

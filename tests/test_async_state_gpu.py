@@ -265,3 +265,107 @@ def test_graph_replay_matches_eager_bitwise():
     assert graphs.captures == 1 and graphs.replays == 4 and graphs.fallbacks == 2
     assert torch.equal(bits(graphed.key_cache), bits(eager.key_cache))
     assert torch.equal(bits(graphed.value_cache), bits(eager.value_cache))
+
+
+# ---------------------------------------------------------------- device tables
+@pytest.mark.parametrize("use_uva", [True, False])
+def test_device_tables_follow_growth_and_slot_reuse(use_uva):
+    """The device tables hold every leased request's pages; a step ships only entries the device lacks."""
+    from vllm_rlt_amd import KVCacheManager
+    from vllm_rlt_amd.async_state import AsyncState
+
+    cache = KVCacheManager(
+        num_layers=1, num_kv_heads=2, head_dim=64, num_blocks=200, block_size=16, max_loops=4, device="cuda",
+        dtype=torch.bfloat16, incremental_allocation=True,
+    )
+    state = AsyncState(cache, CONFIG, SCHEDULER, rows=4, use_uva=use_uva)
+    assert cache.allocate("a", 200, initial_tokens=40) and cache.allocate("b", 200, initial_tokens=1)
+    requests = {"a": Request("a"), "b": Request("b")}
+
+    def check():
+        torch.cuda.synchronize()
+        for rid, slot in state.slots.items():
+            for plane, table in enumerate(cache._get_allocation(rid).block_tables):
+                assert state.tables[slot, plane, : len(table)].tolist() == list(table), (rid, plane)
+
+    bank, _ = state.prepare([requests["a"], requests["b"]], [0, 1], [39, 0], 2, recurrent=True)
+    assert bank.n_patches == 4 * (3 + 1)  # every plane of both tables, once
+    bank.transfer()
+    bank.record_done()
+    check()
+    for step, position in enumerate(range(1, 60, 7)):
+        grew = -(-(position + 1) // 16) - len(cache._get_allocation("b").block_tables[0])
+        assert cache.ensure_capacity("b", position + 1)
+        bank, _ = state.prepare([requests["a"], requests["b"]], [2, 3], [39, position], 2, recurrent=True)
+        assert bank.n_patches == 4 * max(grew, 0)  # only the new pages of "b"
+        bank.transfer()
+        bank.record_done()
+        check()
+    # "a" leaves; "c" takes its slot and ships its whole table.
+    state.release("a")
+    cache.free("a")
+    assert cache.allocate("c", 100, initial_tokens=33)
+    requests["c"] = Request("c")
+    bank, _ = state.prepare([requests["c"], requests["b"]], [0, 0], [32, 5], 2, recurrent=True)
+    assert state.slots["c"] == 0 and bank.n_patches == 4 * 3
+    bank.transfer()
+    bank.record_done()
+    check()
+    # A stale owner is refused: the same id from another request object.
+    with pytest.raises(RuntimeError, match="earlier owner"):
+        state.prepare([Request("c")], [0], [0], 1)
+
+
+# ---------------------------------------------------------------- graphs across layouts
+@pytest.mark.parametrize("layout", ["last_exited", "shared"])
+def test_routed_graph_replays_match_eager_across_layouts_and_depths(layout):
+    """tests/test_cuda_graph.py:29-72 (backend x async x layout): routed, padded batches at depths above 0."""
+    global EMB
+    from vllm_rlt_amd import KVCacheManager
+    from vllm_rlt_amd.async_state import AsyncState
+    from vllm_rlt_amd.graphs import RecurrentGraphs
+
+    def fresh():
+        cache = KVCacheManager(
+            num_layers=3, num_kv_heads=2, head_dim=64, num_blocks=96, block_size=16, max_loops=4, device="cuda",
+            dtype=torch.bfloat16, layout=layout,
+        )
+        cache.key_cache.zero_()
+        cache.value_cache.zero_()
+        for rid in ("a", "b"):
+            assert cache.allocate(rid, 64)
+        return cache
+
+    cos, sin = rope.rotary_cos_sin(torch.arange(8), 64, 1_000_000.0, torch.bfloat16)
+    EMB = torch.stack([cos, sin], dim=1).cuda()
+    graphed, eager = fresh(), fresh()
+    state = AsyncState(graphed, CONFIG, SimpleNamespace(max_num_seqs=2), rows=4)
+    graphs = RecurrentGraphs(core_fn(3), graphed, max_batch_size=2, max_graphs=1, max_positions=64)
+    core = core_fn(3)
+    requests = [Request("a"), Request("b")]
+    g = torch.Generator().manual_seed(5)
+    # LAST-EXITED rows keep their own depth (their plane holds the history);
+    # SHARED rows loop 1..exit on one position, then move on.
+    depth = [1, 3] if layout == "last_exited" else [0, 0]
+    exits, position = [2, 4], [0, 0]
+    for step in range(10):
+        hidden = torch.randn(2, 512, generator=g).to(torch.bfloat16).cuda()
+        bank, batch = state.prepare(requests, list(depth), list(position), 4, recurrent=True)
+        routed = bank.transfer(batch)  # padded to 4 rows
+        got = graphs.run(hidden, routed)
+        bank.record_done()
+        with torch.inference_mode():
+            expect = core(hidden, eager._prepare_batch(["a", "b"], list(depth), list(position)), eager)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(got), bits(expect)), (layout, step, depth, position)
+        _ = torch.randn(64, 64, device="cuda").sum().item()  # eager work between replays
+        for r in range(2):
+            if layout == "last_exited":
+                position[r] += 1
+            else:
+                depth[r] += 1
+                if depth[r] == exits[r]:
+                    depth[r], position[r] = 0, position[r] + 1
+    assert graphs.captures == 1 and graphs.replays == 10 and graphs.fallbacks == 0
+    assert torch.equal(bits(graphed.key_cache), bits(eager.key_cache))
+    assert torch.equal(bits(graphed.value_cache), bits(eager.value_cache))

@@ -1,6 +1,9 @@
-"""KV pool sizing rules (CPU): overrides, the per-page byte count and buffer budgets.
+"""KV pool sizing rules (CPU): overrides, the page size and the budgeted allocations.
 
-Follows vllm_rlt/core/memory.py:11-129 and vllm_rlt/worker/buffers.py:10-26.
+The override rules follow vllm_rlt/core/memory.py (explicit blocks, explicit
+bytes, CPU default) and tests/test_cdb_runtime.py:269 (budget_blocks refuses
+a budget below one page).  The device costs are this package's own: each
+item must equal what the allocating object reports for the same shape.
 """
 
 from types import SimpleNamespace
@@ -8,7 +11,11 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-from vllm_rlt_amd import memory
+from vllm_rlt_amd import memory, ops
+from vllm_rlt_amd.async_state import AsyncState
+from vllm_rlt_amd.buffers import Workspace
+from vllm_rlt_amd.graphs import StaticBatch
+from vllm_rlt_amd.paged_attention import HipPagedAttention
 
 OURO = SimpleNamespace(
     num_hidden_layers=24, num_key_value_heads=16, num_attention_heads=16, head_dim=128, hidden_size=2048,
@@ -26,10 +33,16 @@ def cache_config(**overrides):
 
 
 SCHED = SimpleNamespace(max_num_seqs=8, max_num_batched_tokens=128)
-EXEC = SimpleNamespace(
-    async_scheduling=False, multi_stream=True, static_buffers=False, pad_to_power_of_two=False, cuda_graphs=False,
-    cuda_graph_memory_reserve_bytes=1 << 30,
-)
+
+
+def execution(**overrides):
+    values = dict(
+        async_scheduling=False, multi_stream=True, static_buffers=False, pad_to_power_of_two=False,
+        cuda_graphs=False, cuda_graph_max_batch_size=128, cuda_graph_max_graphs=16,
+        cuda_graph_memory_reserve_bytes=1 << 30,
+    )
+    values.update(overrides)
+    return SimpleNamespace(**values)
 
 
 def test_ouro_page_is_three_mebibytes():
@@ -39,27 +52,57 @@ def test_ouro_page_is_three_mebibytes():
 
 def test_overrides_and_cpu_default():
     per = memory.bytes_per_block(OURO, 16, 2)
-    assert memory.plan_cache(OURO, cache_config(num_blocks=77), SCHED, EXEC, dtype=torch.bfloat16, device="cpu")[0] == 77
-    blocks, info = memory.plan_cache(
-        OURO, cache_config(kv_cache_memory_bytes=10 * per + per - 1), SCHED, EXEC, dtype=torch.bfloat16, device="cpu"
-    )
-    assert blocks == 10 and info == {"source": "bytes", "bytes_per_block": per}
-    assert memory.plan_cache(OURO, cache_config(), SCHED, EXEC, dtype=torch.bfloat16, device="cpu")[0] == 256
+    plan = dict(dtype=torch.bfloat16, device="cpu")
+    assert memory.plan_cache(OURO, cache_config(num_blocks=77), SCHED, execution(), **plan)[0] == 77
+    blocks, info = memory.plan_cache(OURO, cache_config(kv_cache_memory_bytes=11 * per - 1), SCHED, execution(), **plan)
+    assert blocks == 10 and info["source"] == "bytes" and info["bytes_per_block"] == per
+    assert memory.plan_cache(OURO, cache_config(), SCHED, execution(), **plan)[0] == memory.CPU_DEFAULT_BLOCKS
     with pytest.raises(ValueError, match="no memory remains"):
         memory.budget_blocks(per - 1, per)
+    with pytest.raises(ValueError, match="no memory remains"):
+        memory.budget_blocks(-1, per)
+    with pytest.raises(ValueError, match="backend"):
+        memory.plan_cache(OURO, cache_config(), SCHED, execution(), "torch", **plan)
+    with pytest.raises(ValueError, match="dtype and device"):
+        memory.plan_cache(OURO, cache_config(), SCHED, execution())
 
 
-def test_execution_buffers_follow_the_enabled_features():
+def test_costs_follow_the_enabled_features():
     cfg = cache_config()
-    none = memory.execution_buffer_bytes(OURO, SCHED, cfg, EXEC, 2)
-    static = memory.execution_buffer_bytes(OURO, SCHED, cfg, SimpleNamespace(**{**vars(EXEC), "static_buffers": True}), 2)
-    both = memory.execution_buffer_bytes(
-        OURO, SCHED, cfg, SimpleNamespace(**{**vars(EXEC), "static_buffers": True, "async_scheduling": True}), 2
+    plain = memory.execution_bytes(OURO, SCHED, cfg, execution(), 2)
+    assert set(plain) == {"attention_workspace"}
+    full = memory.execution_bytes(
+        OURO, SCHED, cfg, execution(static_buffers=True, async_scheduling=True, cuda_graphs=True), 2
     )
-    assert none == 0 < static < both
-    # Padding rounds the batch rows up to a power of two.
+    assert set(full) == {
+        "attention_workspace", "static_workspaces", "state_slots", "async_state", "graph_inputs", "graph_reserve",
+    }
+    assert all(v > 0 for v in full.values())
+
+
+def test_costs_equal_what_each_object_reports():
+    cfg = cache_config()
+    width = 65536 // 16
+    costs = memory.execution_bytes(
+        OURO, SCHED, cfg, execution(static_buffers=True, async_scheduling=True, cuda_graphs=True), 2
+    )
+    rows = SCHED.max_num_batched_tokens
+    decode = ops.decode_workspace_bytes(rows, 16, 16, 128)
+    assert costs["attention_workspace"] == HipPagedAttention.workspace_size_for(decode) >= decode
+    assert costs["static_workspaces"] == 4 * Workspace.device_bytes(rows, width, 2048, 2)
+    assert costs["async_state"] == AsyncState.device_bytes(8, rows, 2048, width, 4, 2)
+    assert costs["graph_inputs"] == 16 * (StaticBatch.device_bytes(128, width) + 128 * 2048 * 2)
+    # SHARED stores one plane: smaller device tables.
+    shared = memory.execution_bytes(OURO, SCHED, cache_config(layout="shared"), execution(async_scheduling=True), 2)
+    assert shared["async_state"] == AsyncState.device_bytes(8, rows, 2048, width, 1, 2) < costs["async_state"]
+
+
+def test_padding_rounds_rows_up_and_fp32_budgets_the_per_token_prefill():
+    cfg = cache_config()
     odd = SimpleNamespace(max_num_seqs=8, max_num_batched_tokens=100)
-    padded = SimpleNamespace(**{**vars(EXEC), "static_buffers": True, "pad_to_power_of_two": True})
-    assert memory.execution_buffer_bytes(OURO, odd, cfg, padded, 2) == memory.execution_buffer_bytes(
-        OURO, SCHED, cfg, padded, 2
-    )
+    padded = execution(static_buffers=True, pad_to_power_of_two=True)
+    assert memory.execution_bytes(OURO, odd, cfg, padded, 2) == memory.execution_bytes(OURO, SCHED, cfg, padded, 2)
+    fp32 = memory.execution_bytes(OURO, SCHED, cfg, execution(), 4)["attention_workspace"]
+    prefill = ops.prefill_workspace_bytes(128, 8, 4096, 16, 16, 128, 16, torch.float32)
+    assert fp32 >= prefill > 0
+    assert ops.prefill_workspace_bytes(128, 8, 4096, 16, 16, 128, 16, torch.bfloat16) == 0

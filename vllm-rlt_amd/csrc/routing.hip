@@ -62,6 +62,18 @@ __global__ __launch_bounds__(kThreads) void scatter_rows_kernel(RowCopyArgs a) {
   reinterpret_cast<U*>(a.dst + slot * a.dst_stride)[col] = reinterpret_cast<const U*>(a.src + row * a.src_stride)[col];
 }
 
+// grid ceil(n / kThreads): tables[index_i] = value_i for the (index, value)
+// int64 pairs i < n.  The pairs may sit in pinned host memory, read in place.
+// An index outside [0, table_elems) is skipped.
+__global__ __launch_bounds__(kThreads) void patch_tables_kernel(const int64_t* patches, int64_t n, int32_t* tables,
+                                                                int64_t table_elems) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int64_t index = patches[2 * i];
+  if (index < 0 || index >= table_elems) return;
+  tables[index] = static_cast<int32_t>(patches[2 * i + 1]);
+}
+
 int unit_bytes(const void* p, const void* q, int64_t s0, int64_t s1, int64_t row_bytes) {
   const uintptr_t bits = reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(q) |
                          static_cast<uintptr_t>(s0) | static_cast<uintptr_t>(s1) | static_cast<uintptr_t>(row_bytes);
@@ -132,4 +144,16 @@ extern "C" int rlt_scatter_rows(const void* values, int64_t values_row_bytes_str
   a.count = count;
   const int unit = unit_bytes(values, pool, values_row_bytes_stride, pool_row_bytes_stride, row_bytes);
   return launch_rows<false>(a, count, row_bytes, unit, as_stream(stream), "rlt_scatter_rows");
+}
+
+extern "C" int rlt_patch_tables(const int64_t* patches, int64_t n, int32_t* tables, int64_t table_elems,
+                                void* stream) {
+  if (n < 0 || table_elems < 0) return fail(RLT_EINVAL, "rlt_patch_tables: n and table_elems must be >= 0");
+  if (n == 0) return RLT_OK;
+  if (!patches || !tables) return fail(RLT_EINVAL, "rlt_patch_tables: NULL pointer argument");
+  const int64_t blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_patch_tables: too many patches");
+  hipLaunchKernelGGL(patch_tables_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, as_stream(stream),
+                     patches, n, tables, table_elems);
+  return check_launch("rlt_patch_tables");
 }

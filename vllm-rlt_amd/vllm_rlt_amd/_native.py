@@ -54,6 +54,7 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p],
     ),
+    "rlt_patch_tables": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "rlt_kv_export_pages": (
         c_int,
         [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p],

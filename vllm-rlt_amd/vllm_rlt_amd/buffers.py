@@ -14,8 +14,8 @@ arguments, padding and ownership rules:
 * the host side waits for the event of the previous step's last reader
   before it overwrites the pinned inputs (``acquire`` / ``release``).
 
-``execution_buffer_bytes`` (:10-26) lives in memory.py with the rest of the
-capacity planner and is re-exported here.
+Workspace.device_bytes gives the device memory one Workspace holds, which the
+capacity planner (memory.py) budgets.
 """
 
 from __future__ import annotations
@@ -23,10 +23,9 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .memory import execution_buffer_bytes
 from .page_book import PreparedKVBatch
 
-__all__ = ["Workspace", "execution_buffer_bytes"]
+__all__ = ["Workspace"]
 
 _INT64 = ("tokens", "positions", "blocks", "offsets")
 _INT32 = ("tables", "lengths")
@@ -47,6 +46,11 @@ class Workspace:
             kind = torch.int32 if name in _INT32 else torch.int64
             self.host[name] = torch.empty(shape, dtype=kind, pin_memory=pinned)
             self.gpu[name] = torch.empty(shape, dtype=kind, device=device)
+
+    @staticmethod
+    def device_bytes(rows: int, width: int, hidden_size: int, element_size: int) -> int:
+        """Device memory of one Workspace: hidden rows, four int64 and two int32 fields."""
+        return rows * (hidden_size * element_size + 4 * 8 + 4 + 4 * width)
 
     def acquire(self) -> None:
         """Wait for the last reader of the previous step's inputs (buffers.py:49-51)."""

@@ -1,141 +1,175 @@
-"""Startup KV pool sizing for the hip backend.
+"""KV pool sizing for the hip backend.
 
-Mirrors vllm_rlt/core/memory.py:11-129 (budget_blocks, plan_cache) and
-vllm_rlt/worker/buffers.py:10-26 (execution_buffer_bytes): explicit block or
-byte overrides first; otherwise a peak-memory probe on the device, then the
-free memory under gpu_memory_utilization minus the probe's peak (doubled for
-concurrent streams), the runner's static buffers, dynamic metadata, the
-configured reserve and the graph reserve, clamped to the blocks all
-concurrent full-context requests could use.
+Keeps the entry points the engine and tests call (plan_cache, budget_blocks:
+vllm_rlt/engine/llm_engine.py:48-50, tests/test_cdb_runtime.py:269) and the
+reference's override rules (vllm_rlt/core/memory.py): an explicit block count
+or byte budget wins, and a CPU device gets a fixed default.
 
-The probe itself -- a full-depth forward of the model over a temporary KV
-manager -- belongs to the model, which is outside this package: the caller
-passes it as `probe(cache, request_ids, positions)`.  In place of the torch
-backend's long-context attention scratch, the hip backend budgets its own
-decode workspace (split partials for the largest decode batch).
+The device budget is this package's own.  It adds up what will actually be
+allocated next to the pool, asking each allocating object for its size:
+
+* the attention backend's grow-only workspace at its final size
+  (HipPagedAttention.workspace_size_for over rlt_paged_decode_workspace_bytes
+  for the largest decode batch and rlt_paged_prefill_workspace_bytes for the
+  per-token prefill path, which only non-MFMA dtypes take);
+* the runner's static Workspaces and slot pool, and the AsyncState pools and
+  routing banks (their device_bytes());
+* per captured graph its StaticBatch, plus the configured graph reserve for
+  the graphs' private activations;
+* the model's activation peak, measured around a caller-supplied probe
+  (doubled when the core and boundary streams overlap);
+* the configured memory reserve.
+
+The pool gets the rest of min(free memory, utilisation x total - reserved),
+in whole pages, and never more pages than every concurrent request could use.
 """
 
 from __future__ import annotations
 
-import math
+from dataclasses import asdict, dataclass, field
 
 import torch
 
 from . import ops
+from .async_state import AsyncState
+from .buffers import Workspace
+from .graphs import StaticBatch
+from .paged_attention import HipPagedAttention
+
+CPU_DEFAULT_BLOCKS = 256  # vllm_rlt/core/memory.py: pools on a CPU device
 
 
 def budget_blocks(available_bytes: int, bytes_per_block: int) -> int:
-    """Whole blocks that fit in available_bytes (vllm_rlt/core/memory.py:11-18)."""
-    blocks = int(available_bytes) // bytes_per_block
+    """Whole pages of bytes_per_block in available_bytes; at least one, else ValueError."""
+    blocks = int(available_bytes) // int(bytes_per_block)
     if blocks < 1:
         raise ValueError("no memory remains for KV blocks; reduce execution limits or memory reserve")
     return blocks
 
 
-def execution_buffer_bytes(config, scheduler, cache, execution, element_size: int) -> int:
-    """Static runner workspaces and async routing banks (vllm_rlt/worker/buffers.py:10-26)."""
-    rows = scheduler.max_num_batched_tokens
-    if execution.pad_to_power_of_two:
-        rows = 1 << (rows - 1).bit_length()
-    width = math.ceil(config.max_position_embeddings / cache.block_size)
-    hidden = config.hidden_size * element_size
-    total = 0
-    if execution.static_buffers:
-        total += 4 * rows * (hidden + 4 * width + 36) + scheduler.max_num_seqs * hidden
-    if execution.async_scheduling:
-        planes = config.total_ut_steps if cache.layout == "last_exited" else 1
-        total += 4 * rows * (hidden + 4 * width + 68)
-        total += scheduler.max_num_seqs * (hidden + 8 + planes * width * 4)
-        total += 2 * scheduler.max_num_seqs * 24
-    return total
-
-
 def bytes_per_block(config, block_size: int, element_size: int) -> int:
-    """K and V of one page at every layer (vllm_rlt/core/memory.py:24-32)."""
+    """K and V of one page at every layer."""
     return 2 * config.num_hidden_layers * block_size * config.num_key_value_heads * config.head_dim * element_size
 
 
+def _pow2(n: int) -> int:
+    return 1 << (max(int(n), 1) - 1).bit_length()
+
+
+@dataclass
+class MemoryPlan:
+    """Where the device memory goes, in bytes; `costs` are the non-KV allocations."""
+
+    source: str
+    bytes_per_block: int
+    num_blocks: int = 0
+    costs: dict = field(default_factory=dict)
+    budget_bytes: int = 0  # min(free, utilisation x total - reserved) before costs
+    kv_bytes: int = 0  # what remains for pages
+    max_useful_blocks: int = 0
+
+    def as_dict(self) -> dict:
+        return asdict(self)
+
+
+def execution_bytes(config, scheduler, cache, execution, element_size: int, num_q_heads=None) -> dict:
+    """Device bytes of everything the runner and this package allocate beside the pool."""
+    page = cache.block_size
+    width = -(-config.max_position_embeddings // page)
+    rows = scheduler.max_num_batched_tokens
+    if execution.pad_to_power_of_two:
+        rows = _pow2(rows)
+    hidden = config.hidden_size
+    planes = config.total_ut_steps if cache.layout == "last_exited" else 1
+    heads = num_q_heads or config.num_attention_heads
+    costs = {}
+    # One backend workspace serves decode partials and the per-token prefill path.
+    decode = ops.decode_workspace_bytes(rows, heads, config.num_key_value_heads, config.head_dim)
+    prefill = 0
+    if element_size == 4:  # fp32 pools take the per-token prefill path
+        prefill = ops.prefill_workspace_bytes(
+            rows, scheduler.max_num_seqs, width, heads, config.num_key_value_heads, config.head_dim, page,
+            torch.float32,
+        )
+    costs["attention_workspace"] = HipPagedAttention.workspace_size_for(max(decode, prefill))
+    if execution.static_buffers:
+        costs["static_workspaces"] = 4 * Workspace.device_bytes(rows, width, hidden, element_size)
+        costs["state_slots"] = scheduler.max_num_seqs * hidden * element_size
+    if execution.async_scheduling:
+        costs["async_state"] = AsyncState.device_bytes(
+            scheduler.max_num_seqs, rows, hidden, width, planes, element_size
+        )
+    if execution.cuda_graphs:
+        graph_rows = min(execution.cuda_graph_max_batch_size, rows)
+        costs["graph_inputs"] = execution.cuda_graph_max_graphs * (
+            StaticBatch.device_bytes(graph_rows, width) + graph_rows * hidden * element_size
+        )
+        costs["graph_reserve"] = execution.cuda_graph_memory_reserve_bytes
+    return costs
+
+
+def _measure_probe(probe, device) -> int:
+    """Peak bytes allocated above the current level while probe() runs."""
+    torch.cuda.synchronize(device)
+    base = torch.cuda.memory_allocated(device)
+    torch.cuda.reset_peak_memory_stats(device)
+    probe()
+    torch.cuda.synchronize(device)
+    return max(0, torch.cuda.max_memory_allocated(device) - base)
+
+
 @torch.inference_mode()
-def plan_cache(config, cache, scheduler, execution, *, dtype: torch.dtype, device, probe=None, memory_info=None):
-    """(num_blocks, details) for a KV pool of `config`'s shape on `device`.
+def plan_cache(config_or_model, cache, scheduler, execution, backend: str = "hip", *, dtype=None, device=None,
+               probe=None, memory_info=None):
+    """(num_blocks, plan dict) for a KV pool on `device`.
 
-    `cache` carries the reference's CacheConfig fields (num_blocks,
-    kv_cache_memory_bytes, block_size, layout, gpu_memory_utilization,
-    memory_reserve_bytes).  `memory_info` overrides (free, total) device
-    bytes; by default they are read from the device after the allocator's
-    cache is emptied.
+    The first argument is a model (its .config, parameter dtype and device are
+    used) or a config with dtype/device given.  `cache` carries the
+    reference's CacheConfig fields (num_blocks, kv_cache_memory_bytes,
+    block_size, layout, gpu_memory_utilization, memory_reserve_bytes).
+    `probe()` runs the model's largest step; its allocation peak is budgeted.
+    `memory_info` overrides the device's (free, total) bytes.
     """
-    from .kv_cache_manager import KVCacheManager
-
+    if backend != "hip":
+        raise ValueError("unknown attention backend")
+    config = getattr(config_or_model, "config", config_or_model)
+    if hasattr(config_or_model, "parameters"):
+        parameter = next(config_or_model.parameters())
+        dtype = dtype or parameter.dtype
+        device = device or parameter.device
+    if dtype is None or device is None:
+        raise ValueError("plan_cache needs a model, or dtype and device")
     device = torch.device(device)
     element = torch.empty((), dtype=dtype).element_size()
     per_block = bytes_per_block(config, cache.block_size, element)
     if cache.num_blocks is not None:
-        return cache.num_blocks, {"source": "blocks", "bytes_per_block": per_block}
+        plan = MemoryPlan("blocks", per_block, num_blocks=cache.num_blocks)
+        return plan.num_blocks, plan.as_dict()
     if cache.kv_cache_memory_bytes is not None:
-        return budget_blocks(cache.kv_cache_memory_bytes, per_block), {"source": "bytes", "bytes_per_block": per_block}
+        plan = MemoryPlan("bytes", per_block, num_blocks=budget_blocks(cache.kv_cache_memory_bytes, per_block))
+        return plan.num_blocks, plan.as_dict()
     if device.type != "cuda":
-        return 256, {"source": "cpu_default", "bytes_per_block": per_block}
-    torch.cuda.synchronize(device)
-    with torch.cuda.device(device):
-        torch.cuda.empty_cache()
-    free_before, total = memory_info if memory_info is not None else torch.cuda.mem_get_info(device)
-    reserved = torch.cuda.memory_reserved(device)
-    allocated = torch.cuda.memory_allocated(device)
-    torch.cuda.reset_peak_memory_stats(device)
-    count = min(scheduler.max_num_batched_tokens, scheduler.max_num_seqs * config.max_position_embeddings)
-    if execution.pad_to_power_of_two:
-        count = 1 << (count - 1).bit_length()
-    peak = 0
+        plan = MemoryPlan("cpu_default", per_block, num_blocks=CPU_DEFAULT_BLOCKS)
+        return plan.num_blocks, plan.as_dict()
+
+    costs = execution_bytes(config, scheduler, cache, execution, element)
     if probe is not None:
-        lengths = [
-            min(config.max_position_embeddings, count - start)
-            for start in range(0, count, config.max_position_embeddings)
-        ]
-        probe_cache = KVCacheManager(
-            num_layers=config.num_hidden_layers,
-            num_kv_heads=config.num_key_value_heads,
-            head_dim=config.head_dim,
-            max_loops=config.total_ut_steps,
-            num_blocks=sum(math.ceil(n / cache.block_size) for n in lengths) * config.total_ut_steps,
-            block_size=cache.block_size,
-            device=device,
-            dtype=dtype,
-        )
-        ids, positions = [], []
-        for index, length in enumerate(lengths):
-            rid = f"profile-{index}"
-            probe_cache.allocate(rid, length)
-            ids.extend([rid] * length)
-            positions.extend(range(length))
-        probe(probe_cache, ids, positions)
+        peak = _measure_probe(probe, device)
+        overlap = execution.async_scheduling and execution.multi_stream
+        costs["activation_peak"] = peak * (2 if overlap else 1)
+    costs["reserve"] = cache.memory_reserve_bytes
+    if memory_info is None:
         torch.cuda.synchronize(device)
-        peak = max(0, torch.cuda.max_memory_allocated(device) - allocated)
-        del probe_cache
-    # The hip decode keeps split partials for every row of the largest batch.
-    workspace = ops.decode_workspace_bytes(
-        count, config.num_attention_heads, config.num_key_value_heads, config.head_dim
+        with torch.cuda.device(device):
+            torch.cuda.empty_cache()  # cached but unused segments count as free
+        memory_info = torch.cuda.mem_get_info(device)
+    free, total = memory_info
+    budget = min(int(free), int(total * cache.gpu_memory_utilization) - torch.cuda.memory_reserved(device))
+    kv_bytes = budget - sum(costs.values())
+    planes = config.total_ut_steps if cache.layout == "last_exited" else 1
+    useful = -(-config.max_position_embeddings // cache.block_size) * planes * scheduler.max_num_seqs
+    plan = MemoryPlan(
+        "device_profile", per_block, num_blocks=min(budget_blocks(kv_bytes, per_block), useful), costs=costs,
+        budget_bytes=budget, kv_bytes=kv_bytes, max_useful_blocks=useful,
     )
-    buffers = execution_buffer_bytes(config, scheduler, cache, execution, element)
-    metadata = scheduler.max_num_batched_tokens * math.ceil(config.max_position_embeddings / cache.block_size) * 4
-    budget = min(free_before, int(total * cache.gpu_memory_utilization) - reserved)
-    concurrent_peak = peak * (2 if execution.async_scheduling and execution.multi_stream else 1)
-    graph_reserve = execution.cuda_graph_memory_reserve_bytes if execution.cuda_graphs else 0
-    budget -= concurrent_peak + workspace + buffers + metadata + cache.memory_reserve_bytes + graph_reserve
-    useful_blocks = (
-        math.ceil(config.max_position_embeddings / cache.block_size)
-        * (config.total_ut_steps if cache.layout == "last_exited" else 1)
-        * scheduler.max_num_seqs
-    )
-    blocks = min(budget_blocks(budget, per_block), useful_blocks)
-    return blocks, dict(
-        source="device_profile",
-        bytes_per_block=per_block,
-        profile_peak_bytes=peak,
-        concurrent_peak_bytes=concurrent_peak,
-        max_useful_blocks=useful_blocks,
-        graph_reserve_bytes=graph_reserve,
-        static_buffer_bytes=buffers,
-        decode_workspace_bytes=workspace,
-        kv_budget_bytes=int(budget),
-    )
+    return plan.num_blocks, plan.as_dict()

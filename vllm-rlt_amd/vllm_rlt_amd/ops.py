@@ -222,6 +222,30 @@ def scatter_rows(values: torch.Tensor, slots: torch.Tensor, pool: torch.Tensor, 
     check(rc, "rlt_scatter_rows")
 
 
+def patch_tables(patches: torch.Tensor, count: int, tables: torch.Tensor) -> None:
+    """tables.view(-1)[patches[i, 0]] = patches[i, 1] for i < count (rlt_patch_tables).
+
+    patches: contiguous int64 [n, 2] on the tables' device or in pinned host
+    memory (read in place); indices distinct.  tables: contiguous int32.
+    """
+    device = _require_rocm(tables)
+    if patches.dtype != torch.int64 or patches.ndim != 2 or patches.shape[1] != 2 or not patches.is_contiguous():
+        raise ValueError("patches must be contiguous int64 [n, 2]")
+    if patches.device.type == "cpu":
+        if not patches.is_pinned():
+            raise ValueError("host patches must be pinned")
+    elif patches.device != device:
+        raise ValueError("patches must be pinned host memory or on the tables' device")
+    if tables.dtype != torch.int32 or not tables.is_contiguous():
+        raise ValueError("tables must be contiguous int32")
+    if not 0 <= count <= patches.shape[0]:
+        raise ValueError("count exceeds the patch rows")
+    check(
+        _native.load().rlt_patch_tables(patches.data_ptr(), count, tables.data_ptr(), tables.numel(), stream_handle(device)),
+        "rlt_patch_tables",
+    )
+
+
 def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
     """Bytes of split-K partials rlt_paged_decode needs for a batch of n_rows (shape only)."""
     return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))

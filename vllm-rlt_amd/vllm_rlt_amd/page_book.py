@@ -495,6 +495,17 @@ class KVPageBook:
         plan = self._plan_batch(request_ids, depths, positions, for_write=for_write, packed_prefill=packed_prefill)
         return self._batch_from_plan(plan)
 
+    def _require_history(self, batch: PreparedKVBatch) -> None:
+        """Every row's earlier positions hold KV at every layer (a whole-core replay's precondition)."""
+        for allocation, depth, position in batch.rows:
+            for layer in range(self.num_layers):
+                self._require_prefix(allocation, layer, depth, position)
+
+    def _record_all_layers(self, batch: PreparedKVBatch) -> None:
+        """Mark every row's position written at every layer (after a whole-core replay)."""
+        for layer in range(self.num_layers):
+            self._record_written(batch, layer)
+
     def _record_written(self, batch: PreparedKVBatch, layer: int) -> None:
         for allocation, depth, position in batch.rows:
             allocation.written[self._plane(depth)][layer].add(position)

@@ -71,13 +71,17 @@ class HipPagedAttention:
     def workspace_bytes(self) -> int:
         return 0 if self._workspace is None else self._workspace.numel()
 
+    @staticmethod
+    def workspace_size_for(nbytes: int) -> int:
+        """Size the workspace grows to for a need of nbytes: a power of two, 1 MiB or more."""
+        return 1 << max(20, (max(int(nbytes), 1) - 1).bit_length())
+
     def reserve(self, nbytes: int) -> torch.Tensor:
-        """The workspace, grown to at least nbytes (a power of two, 1 MiB or more)."""
-        nbytes = int(nbytes)
-        if self._workspace is None or self._workspace.numel() < nbytes:
+        """The workspace, grown to at least nbytes."""
+        if self._workspace is None or self._workspace.numel() < int(nbytes):
             if self._workspace is not None:
                 self._outgrown.append(self._workspace)
-            size = 1 << max(20, (max(nbytes, 1) - 1).bit_length())
+            size = self.workspace_size_for(nbytes)
             self._workspace = torch.empty(size, dtype=torch.uint8, device=self.device)
         return self._workspace
 
