@@ -392,19 +392,55 @@ def iqr(values):
     return [round(q[0], 5), round(q[2], 5)]
 
 
-def cpu_baseline(w, step, reps):
-    """The CPU oracle (op-for-op restatement of the reference CPU path) on one layer-step.
+def usable_cpus():
+    """Cores this process may run on: its affinity mask, limited by a cgroup CPU quota if one is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if quota != "max":
+            n = min(n, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return n
 
-    Sample: every row of the workload at `step`, one layer: index_put-style KV
+
+def cpu_description(threads):
+    """Host facts reported beside a CPU baseline."""
+    model = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "cpu_model": model,
+        "os_cpu_count": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+        "torch_threads": threads,
+    }
+
+
+def cpu_baseline(w, step, reps):
+    """The CPU oracle (op-for-op restatement of the reference CPU path) on one loop-step.
+
+    Sample: every row of the workload at `step`.  The host metadata build of
+    the loop-step (_prepare_batch: write addresses, -1-padded tables, lengths,
+    kv_cache_manager.py:398-478) once, then one layer-step: index_put-style KV
     append plus paged attention over a 1-layer host copy of exactly the pages
-    those rows reference.  loop-steps/s = 1 / (24 * median layer-step time).
+    those rows reference.  loop-steps/s = 1 / (metadata + 24 * layer-step),
+    medians, with every core the process may use.
     """
     from oracle import kv_ops
     from oracle.paged_attention import paged_attention_cpu
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = usable_cpus()
     torch.set_num_threads(threads)
     torch.cuda.synchronize()
+    desc = w.descriptors_host[step].tolist()
+    host_tables = [tuple(w.tables_host[slot, plane].tolist()) for slot, plane, _ in desc]
+    host_positions = [pos for _, _, pos in desc]
     lengths = w.lengths.cpu()
     tables = w.row_tables.cpu()
     need = sorted({int(b) for r in range(w.batch) for b in tables[r, : math.ceil(int(lengths[r]) / PAGE)]})
@@ -417,29 +453,39 @@ def cpu_baseline(w, step, reps):
     blocks = remap[w.blocks.cpu()]
     offsets = w.offsets.cpu()
     q, k_new, v_new = w.q[0].cpu(), w.k_new[0].cpu(), w.v_new[0].cpu()
-    def layer_time(reps):
+    def median_time(fn, reps):
         times = []
         for _ in range(reps + 1):
             t0 = time.perf_counter()
-            kv_ops.append(kc, vc, 0, blocks, offsets, k_new, v_new)
-            paged_attention_cpu(q, kc[:, 0], vc[:, 0], local, lengths)
+            fn()
             times.append(time.perf_counter() - t0)
         return statistics.median(times[1:])
 
-    layer_s = layer_time(reps)
+    def metadata():
+        b, o, t, n = kv_ops.prepare_addresses(host_tables, host_positions, PAGE)
+        return torch.from_numpy(b), torch.from_numpy(o), torch.from_numpy(t), torch.from_numpy(n)
+
+    def layer():
+        kv_ops.append(kc, vc, 0, blocks, offsets, k_new, v_new)
+        paged_attention_cpu(q, kc[:, 0], vc[:, 0], local, lengths)
+
+    meta_s = median_time(metadata, reps)
+    layer_s = median_time(layer, reps)
     torch.set_num_threads(1)
-    single_s = layer_time(1)
+    single_s = median_time(layer, 1)
     torch.set_num_threads(threads)
+    loop_s = meta_s + LAYERS * layer_s
     return {
-        "value": 1.0 / (LAYERS * layer_s),
+        "value": 1.0 / loop_s,
         "unit": "loop-steps/s",
         "cores": threads,
         "kind": "port",
-        "single_thread_value": 1.0 / (LAYERS * single_s),
-        "sample": f"one layer-step (all {w.batch} rows, 1 layer, append + attention), median of {reps} "
-        f"after 1 warmup, extrapolated x{LAYERS} layers; {layer_s * 1e3:.1f} ms/layer-step on {threads} "
-        f"threads, {single_s * 1e3:.1f} ms on 1 thread (1 run after 1 warmup); "
-        f"cpu={platform.processor() or platform.machine()}",
+        "single_thread_value": 1.0 / (meta_s + LAYERS * single_s),
+        **cpu_description(threads),
+        "sample": f"one loop-step of all {w.batch} rows: the host metadata build ({meta_s * 1e3:.2f} ms) plus "
+        f"one layer-step (append + attention, 1-layer pool) extrapolated x{LAYERS} layers; "
+        f"{layer_s * 1e3:.1f} ms/layer-step on {threads} threads (median of {reps} after 1 warmup), "
+        f"{single_s * 1e3:.1f} ms on 1 thread (1 run after 1 warmup)",
     }
 
 
@@ -548,7 +594,7 @@ def prefill_cpu_baseline(w, reps, stride=32):
     """
     from oracle.paged_attention import paged_attention_cpu
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = usable_cpus()
     torch.set_num_threads(threads)
     chunk = PREFILL["chunk"]
     tables = w.depth_tables[0].cpu()
@@ -588,9 +634,10 @@ def prefill_cpu_baseline(w, reps, stride=32):
         "cores": threads,
         "kind": "port",
         "single_thread_value": flops / t_single / 1e12,
+        **cpu_description(threads),
         "sample": f"{len(rows)} query rows (1 in {stride} of each 512-token chunk, depth 0, layer 0, "
         f"{sum(row_lens)} visible keys), median of {reps} after 1 warmup: {t_multi * 1e3:.1f} ms on {threads} "
-        f"threads, {t_single * 1e3:.1f} ms on 1 thread; cpu={platform.processor() or platform.machine()}",
+        f"threads, {t_single * 1e3:.1f} ms on 1 thread",
     }
 
 
