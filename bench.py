@@ -81,6 +81,12 @@ def parse_args():
         help="decode workloads: capture one loop-step in a HIP graph and time its replays",
     )
     p.add_argument(
+        "--append",
+        choices=["fused", "separate"],
+        default="fused",
+        help="decode workloads: KV append fused into the decode launch, or its own launch before it",
+    )
+    p.add_argument(
         "--calibrate-counters",
         action="store_true",
         help="only run one 1 GiB device-to-device copy (known-size kernel for scaling HBM counters)",
@@ -282,6 +288,7 @@ class Workload:
         )
         # Every row's table begins with the aliased prefix pages: the decode reads
         # them once per launch for all rows (rlt_paged_decode_shared_prefix).
+        self.fused_append = True  # KV append inside the decode launch (no shared-prefix hint)
         self.prefix_hint = None
         if self.shared_pages.numel():
             self.prefix_hint = ops.shared_prefix(
@@ -317,8 +324,20 @@ def build_metadata(w, step, descriptors=None):
 
 
 def layer_step(w, layer):
+    """KV append then decode attention of one layer.
+
+    Every row is a different request (or a request at one depth), so no row
+    reads a slot another row writes: one fused launch unless the batch carries
+    the shared-prefix hint, which the fused launch does not take.
+    """
     from vllm_rlt_amd import ops
 
+    if w.prefix_hint is None and w.fused_append:
+        ops.paged_decode_append(
+            w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths, w.k_new[layer],
+            w.v_new[layer], w.blocks, w.offsets, out=w.out[layer], workspace=w.workspace,
+        )
+        return
     ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
     ops.paged_decode(
         w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
@@ -749,6 +768,7 @@ def main():
     total = args.warmup + args.steps
     t_setup = time.perf_counter()
     w = Workload(args.workload, total, args.seed, device)
+    w.fused_append = args.append == "fused" and w.prefix_hint is None
     torch.cuda.synchronize()
     print(
         f"[bench] workload {args.workload}: batch {w.batch}, planes {w.planes}, pool "
@@ -805,7 +825,8 @@ def main():
             raise SystemExit("graph replay differs from eager execution")
 
     # Decode-launch timing with HIP events on the launch stream (separate pass,
-    # same steps): each event pair brackets one rlt_paged_decode call.
+    # same steps): each event pair brackets one decode launch, the fused
+    # append-and-decode one when the loop-step uses it.
     from vllm_rlt_amd import ops
 
     stream = torch.cuda.current_stream(device)
@@ -818,19 +839,25 @@ def main():
     for step in range(args.warmup, total):
         build_metadata(w, step)
         for layer in range(LAYERS):
-            ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
+            if not w.fused_append:
+                ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
             start, end = next(events)
             start.record(stream)
-            ops.paged_decode(
-                w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
-                out=w.out[layer], workspace=w.workspace, shared_prefix=w.prefix_hint,
-            )
+            if w.fused_append:
+                layer_step(w, layer)
+            else:
+                ops.paged_decode(
+                    w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
+                    out=w.out[layer], workspace=w.workspace, shared_prefix=w.prefix_hint,
+                )
             end.record(stream)
     torch.cuda.synchronize()
     launch_ms = [s.elapsed_time(e) for s, e in pairs]
     decode_ms = statistics.fmean(launch_ms)
-    decode_avg_bytes = statistics.fmean(decode_bytes)
-    unique_avg_bytes = statistics.fmean(unique_bytes)
+    # The fused launch also moves the new tokens: 8 KiB read + 8 KiB written + 16 B of address per row.
+    fused_extra = w.batch * (4 * HKV * HEAD_DIM * 2 + 16) if w.fused_append else 0
+    decode_avg_bytes = statistics.fmean(decode_bytes) + fused_extra
+    unique_avg_bytes = statistics.fmean(unique_bytes) + fused_extra
     # Aliased prefix pages are read by every row but fetched from HBM about
     # once per launch: the roofline uses the unique bytes.
     achieved = unique_avg_bytes / (decode_ms * 1e-3) / 1e9
@@ -861,13 +888,17 @@ def main():
             "seq_len": int(w.contexts.float().mean().item()),
             "parallelism": "single-gpu",
             "launch": "hip-graph replay" if graph is not None else "eager",
+            "append": "fused into the decode launch" if w.fused_append else "own launch before the decode",
         },
         "hbm_gb_per_s": round(gbs, 1),
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "step_ms_median": round(statistics.median(step_ms), 4),
         "step_ms_iqr": iqr(step_ms),
         "roofline": {
-            "kernel": "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
+            "kernel": "rlt_paged_decode_append (paged_decode_kernel split pass reading each row's new token "
+            "in place + paged_decode_merge_kernel storing it)"
+            if w.fused_append
+            else "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
             if w.prefix_hint is None
             else "rlt_paged_decode_shared_prefix (shared_prefix_kernel + paged_decode_kernel split pass + "
             "paged_decode_merge_kernel)",

@@ -209,6 +209,40 @@ int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_ca
                      int64_t workspace_bytes, void* stream);
 
 /*
+ * KV append and decode attention of one layer in one launch.
+ * Replaces, for a decode batch, the pair _write_prepared then _attend_prepared
+ * (vllm_rlt/core/kv_cache_manager.py:520-534 and 559-586): first
+ *   key_cache[write_blocks[i], write_offsets[i]] = k_new[i]  (and V), i < n_write
+ * on the layer slices, then rlt_paged_decode over the updated pages; the pages
+ * and the output equal that sequence's bit for bit.  Inside the launch a row
+ * whose write slot is its own last token's slot (table[(len-1)/page],
+ * (len-1) % page) reads that token from k_new / v_new, and the pages are
+ * written after every split has read its keys.  So the caller guarantees that
+ * no row reads a slot another row writes in this launch (true of a decode
+ * batch with one row per request and depth; a packed chunk, where a row reads
+ * the tokens of the rows before it, must use rlt_kv_append then
+ * rlt_paged_decode).  Shapes the tiled kernel does not cover, or k_new / v_new
+ * rows that are not 16-byte aligned with a unit dim stride, run the append
+ * first and then the decode.
+ *   key_cache / value_cache: the layer slices, written.
+ *   k_new / v_new: [n_rows or more, num_kv_heads, head_dim], strides (row,
+ *     head, dim) in elements.  write_blocks / write_offsets: device int64
+ *     [n_write]; a slot outside the pool is skipped.  n_write <= n_rows.
+ *   workspace: as rlt_paged_decode.
+ */
+int rlt_paged_decode_append(const void* q, const int64_t* q_strides, void* key_cache,
+                            void* value_cache, const int64_t* kv_strides,
+                            const int32_t* block_tables, int64_t table_stride,
+                            int64_t max_table_width, const int32_t* context_lengths, void* out,
+                            const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                            int64_t num_blocks, float scale, int dtype, const void* k_new,
+                            const int64_t* k_new_strides, const void* v_new,
+                            const int64_t* v_new_strides, const int64_t* write_blocks,
+                            const int64_t* write_offsets, int64_t n_write, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/*
  * rlt_paged_decode without a workspace argument: allocates nothing.
  * No counterpart in the reference.  It is for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses

@@ -125,6 +125,19 @@ struct DecodeArgs {
   const int32_t* prefix_rows;
   const int32_t* prefix_table;
   int n_prefix_rows, prefix_pages, prefix_split_len;
+  // Fused KV append (rlt_paged_decode_append; null / 0 otherwise): row
+  // r < n_write stores its new token k_new[r] / v_new[r] ([hkv, D], strides
+  // in elements, dim stride 1) at slot (write_blocks[r], write_offsets[r]) of
+  // the layer slices.  The split pass reads a row's own new token from
+  // k_new / v_new (its last token, when the write slot is the row's last
+  // token slot) and the merge kernel stores it into the pages after every
+  // split has read them, so no page is written and read in one kernel.
+  const void* k_new;
+  const void* v_new;
+  int64_t kn_row, kn_head, kn_dim, vn_row, vn_head, vn_dim;
+  const int64_t* write_blocks;
+  const int64_t* write_offsets;
+  int n_write;
 };
 
 // A row's effective context length; never reaches past its table row.
@@ -265,7 +278,7 @@ __device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int la
   }
 }
 
-template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX>
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX, bool APPEND>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   using PK = Packet<T>;
   constexpr int EPL = PK::N;      // elements of one token a lane owns
@@ -297,6 +310,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int t_begin = sp * split_len;
     const int t_end = min(len, t_begin + split_len);
     const int last = t_end - 1;
+    // Fused append: the row's write slot, read up front when this is its last split.
+    int64_t wb = -1, wo = -1;
+    if constexpr (APPEND) {
+      if (t_end == len && r < a.n_write) {
+        wb = a.write_blocks[r];
+        wo = a.write_offsets[r];
+      }
+    }
 
     // q for the G query heads of this kv head, pre-scaled into log2 units.
     float qv[G][EPL];
@@ -404,17 +425,54 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
           }
         }
       };
+      // The final tile of a row whose new token is fused in: the lanes of
+      // token len - 1 load it from `fresh_row` (k_new / v_new) instead of the
+      // page slot, within the tile's own load stream.
+      auto issue_fresh = [&](u32x4 (&dst)[NI], const T* base, const T* fresh_row, const int64_t (&blk)[PPT],
+                             int t0) {
+#pragma unroll
+        for (int pg = 0; pg < PPT; ++pg) {
+          const T* page = base + blk[pg] * a.kv_block;
+#pragma unroll
+          for (int i = 0; i < IPP; ++i) {
+            const int tok = min(t0 + pg * P + i * TPI + g, last);
+            const uint32_t off = static_cast<uint32_t>(tok & (P - 1)) * tok_stride + lane_dim;
+            const T* src = tok == len - 1 ? fresh_row + lane_dim : page + off;
+            dst[pg * IPP + i] = *reinterpret_cast<const u32x4*>(src);
+          }
+        }
+      };
       const int ntiles = (c1 - c0 + TILE - 1) / TILE;
+      // Whether this chunk ends the row and the row's write slot is its last
+      // token's slot (page id from the chunk's table entries): then the new
+      // token comes from k_new / v_new.
+      bool fresh = false;
+      const T* kn_row = nullptr;
+      const T* vn_row = nullptr;
+      if constexpr (APPEND) {
+        fresh = c1 == len && wb >= 0 && wo == (len - 1) % P &&
+                wb == static_cast<int64_t>(__builtin_amdgcn_readlane(table_entry, chunk_last));
+        kn_row = static_cast<const T*>(a.k_new) + r * a.kn_row + static_cast<int64_t>(h) * a.kn_head;
+        vn_row = static_cast<const T*>(a.v_new) + r * a.vn_row + static_cast<int64_t>(h) * a.vn_head;
+      }
       u32x4 kp[NI], vp[NI];
       int64_t blk[PPT];
       // sched_barrier keeps every K load of a tile ahead of its V loads in
       // issue order, so waiting for K never waits for V.
       tile_pages(c0, blk);
-      issue(kp, kbase, blk, c0);
-      __builtin_amdgcn_sched_barrier(0);
-      issue(vp, vbase, blk, c0);
+      if (APPEND && fresh && ntiles == 1) {
+        issue_fresh(kp, kbase, kn_row, blk, c0);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_fresh(vp, vbase, vn_row, blk, c0);
+      } else {
+        issue(kp, kbase, blk, c0);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(vp, vbase, blk, c0);
+      }
       int t0 = c0;
-      for (int it = 1; it < ntiles; ++it, t0 += TILE) {
+      // With a fused token the iteration that issues the final tile is peeled.
+      const int steady = (APPEND && fresh) ? ntiles - 1 : ntiles;
+      for (int it = 1; it < steady; ++it, t0 += TILE) {
         float sc[G][NI];
         scores(kp, t0, sc);
         tile_pages(t0 + TILE, blk);
@@ -423,6 +481,19 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         accumulate(vp, t0, sc);
         issue(vp, vbase, blk, t0 + TILE);
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (APPEND) {
+        if (fresh && ntiles > 1) {
+          float sc[G][NI];
+          scores(kp, t0, sc);
+          tile_pages(t0 + TILE, blk);
+          issue_fresh(kp, kbase, kn_row, blk, t0 + TILE);
+          __builtin_amdgcn_sched_barrier(0);
+          accumulate(vp, t0, sc);
+          issue_fresh(vp, vbase, vn_row, blk, t0 + TILE);
+          __builtin_amdgcn_sched_barrier(0);
+          t0 += TILE;
+        }
       }
       float sc[G][NI];
       scores(kp, t0, sc);
@@ -516,13 +587,33 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Merge kernel: one wavefront per (row, kv_head) with more than one split.
+// The fused append's page write of row r's kv head h: 16-byte chunks of the
+// [D] slab from k_new / v_new to (write_blocks[r], write_offsets[r]).  A slot
+// outside the pool is skipped.
+template <typename T, int D>
+__device__ __forceinline__ void store_new_token(const DecodeArgs& a, int r, int h, int lane) {
+  constexpr int kChunks = D * static_cast<int>(sizeof(T)) / 16;
+  static_assert(kChunks <= 64, "one lane per 16-byte chunk");
+  const int64_t b = a.write_blocks[r], o = a.write_offsets[r];
+  if (b < 0 || b >= a.num_blocks || o < 0 || o >= a.page || lane >= kChunks) return;
+  const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head;
+  const T* kn = static_cast<const T*>(a.k_new) + r * a.kn_row + static_cast<int64_t>(h) * a.kn_head;
+  const T* vn = static_cast<const T*>(a.v_new) + r * a.vn_row + static_cast<int64_t>(h) * a.vn_head;
+  reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.k) + slot))[lane] =
+      reinterpret_cast<const u32x4*>(kn)[lane];
+  reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.v) + slot))[lane] =
+      reinterpret_cast<const u32x4*>(vn)[lane];
+}
+
+// Merge kernel: one wavefront per (row, kv_head) with more than one split;
+// with a fused append also the page write of every appending (row, kv_head).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (item >= a.n_rows * a.hkv) return;
   const int r = item / a.hkv;
   const int h = item - r * a.hkv;
+  if (r < a.n_write) store_new_token<T, D>(a, r, h, threadIdx.x & 63);
   int split_len, ns;
   split_plan(row_length(a, r), &split_len, &ns);
   if (ns > 1) merge_partials<T, D>(a, r, h, ns, threadIdx.x & 63);
@@ -799,55 +890,83 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
 // Host dispatch.
 using DecodeKernel = void (*)(DecodeArgs);
 
-template <typename T, int D, bool XCD, bool PREFIX>
+template <typename T, int D, bool XCD, bool PREFIX, bool APPEND>
 DecodeKernel pick_group(int G) {
   switch (G) {
-    case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, PREFIX>;
-    case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, PREFIX>;
-    case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, PREFIX>;
-    case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, PREFIX>;
+    case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, PREFIX, APPEND>;
+    case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, PREFIX, APPEND>;
+    case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, PREFIX, APPEND>;
+    case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, PREFIX, APPEND>;
     default: return nullptr;
   }
+}
+
+// The fused-append split pass is compiled for the XCD-affine schedule without
+// the shared-prefix check; other cases append first, then decode.
+template <typename T, int D, bool PREFIX>
+DecodeKernel pick_group(int G, bool xcd, bool append) {
+  if (append) {
+    if constexpr (!PREFIX) return xcd ? pick_group<T, D, true, false, true>(G) : nullptr;
+    return nullptr;
+  }
+  return xcd ? pick_group<T, D, true, PREFIX, false>(G) : pick_group<T, D, false, PREFIX, false>(G);
 }
 
 // The split pass with the shared-prefix check exists where the prefix pass
 // does (16-bit types, head_dim 128); everywhere else it is compiled out.
 template <typename T, int D>
-DecodeKernel pick_group(int G, bool xcd, bool prefix) {
+DecodeKernel pick_group(int G, bool xcd, bool prefix, bool append) {
   if (prefix) {
-    if constexpr (D == 128 && !std::is_same_v<T, float>)
-      return xcd ? pick_group<T, D, true, true>(G) : pick_group<T, D, false, true>(G);
+    if constexpr (D == 128 && !std::is_same_v<T, float>) return pick_group<T, D, true>(G, xcd, append);
     return nullptr;
   }
-  return xcd ? pick_group<T, D, true, false>(G) : pick_group<T, D, false, false>(G);
+  return pick_group<T, D, false>(G, xcd, append);
 }
 
 template <typename T>
-DecodeKernel pick_tiled(int d, int G, bool xcd, bool prefix);
+DecodeKernel pick_tiled(int d, int G, bool xcd, bool prefix, bool append);
 template <>
-DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd, bool prefix) {
+DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd, bool prefix, bool append) {
   switch (d) {
-    case 64: return pick_group<bf16, 64>(G, xcd, prefix);
-    case 128: return pick_group<bf16, 128>(G, xcd, prefix);
-    case 256: return pick_group<bf16, 256>(G, xcd, prefix);
+    case 64: return pick_group<bf16, 64>(G, xcd, prefix, append);
+    case 128: return pick_group<bf16, 128>(G, xcd, prefix, append);
+    case 256: return pick_group<bf16, 256>(G, xcd, prefix, append);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<f16>(int d, int G, bool xcd, bool prefix) {
+DecodeKernel pick_tiled<f16>(int d, int G, bool xcd, bool prefix, bool append) {
   switch (d) {
-    case 64: return pick_group<f16, 64>(G, xcd, prefix);
-    case 128: return pick_group<f16, 128>(G, xcd, prefix);
-    case 256: return pick_group<f16, 256>(G, xcd, prefix);
+    case 64: return pick_group<f16, 64>(G, xcd, prefix, append);
+    case 128: return pick_group<f16, 128>(G, xcd, prefix, append);
+    case 256: return pick_group<f16, 256>(G, xcd, prefix, append);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<float>(int d, int G, bool xcd, bool prefix) {
+DecodeKernel pick_tiled<float>(int d, int G, bool xcd, bool prefix, bool append) {
   switch (d) {
-    case 64: return pick_group<float, 64>(G, xcd, prefix);
-    case 128: return pick_group<float, 128>(G, xcd, prefix);
+    case 64: return pick_group<float, 64>(G, xcd, prefix, append);
+    case 128: return pick_group<float, 128>(G, xcd, prefix, append);
     default: return nullptr;
+  }
+}
+
+// Unfused append for shapes the fused path does not cover: grid (n_write,
+// hkv), one wave copies row r's head h slab (any dim strides) into its slot.
+template <typename T>
+__global__ __launch_bounds__(64) void slice_append_kernel(DecodeArgs a) {
+  const int r = blockIdx.x, h = blockIdx.y;
+  const int64_t b = a.write_blocks[r], o = a.write_offsets[r];
+  if (b < 0 || b >= a.num_blocks || o < 0 || o >= a.page) return;
+  const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head;
+  T* kd = const_cast<T*>(static_cast<const T*>(a.k)) + slot;
+  T* vd = const_cast<T*>(static_cast<const T*>(a.v)) + slot;
+  const T* kn = static_cast<const T*>(a.k_new) + r * a.kn_row + static_cast<int64_t>(h) * a.kn_head;
+  const T* vn = static_cast<const T*>(a.v_new) + r * a.vn_row + static_cast<int64_t>(h) * a.vn_head;
+  for (int d = threadIdx.x; d < a.d; d += 64) {
+    kd[d * a.kv_dim] = kn[d * a.kn_dim];
+    vd[d * a.kv_dim] = vn[d * a.vn_dim];
   }
 }
 
@@ -892,11 +1011,25 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
                          stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
                          a.kv_token * a.page < (int64_t(1) << 31);
   const bool xcd = RLT_DECODE_XCD_SCHEDULE && a.hkv % kWaves == 0;
-  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, false);
+  if (a.n_write > 0) {
+    // The fused append needs the tiled kernel and 16-byte rows of k_new / v_new;
+    // otherwise the new tokens are written first and the decode runs as usual.
+    const bool fused = layout_ok && !a.prefix_member && a.kn_dim == 1 && a.vn_dim == 1 && aligned16(a.k_new) &&
+                       aligned16(a.v_new) &&
+                       stride16(a.kn_row, esize) && stride16(a.kn_head, esize) && stride16(a.vn_row, esize) &&
+                       stride16(a.vn_head, esize) && pick_tiled<T>(a.d, G, xcd, false, true) != nullptr;
+    if (!fused) {
+      hipLaunchKernelGGL(slice_append_kernel<T>, dim3(a.n_write, a.hkv), dim3(64), 0, stream, a);
+      if (int rc = check_launch("rlt_paged_decode_append(append)")) return rc;
+      a.n_write = 0;
+    }
+  }
+  const bool append = a.n_write > 0;
+  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, false, append);
   if (a.prefix_member && !(tiled && launch_shared_prefix<T>(a, stream))) a.prefix_member = nullptr;
   if (a.prefix_member) {
     if (int rc = check_launch("rlt_paged_decode_shared_prefix(prefix)")) return rc;
-    tiled = pick_tiled<T>(a.d, G, xcd, true);
+    tiled = pick_tiled<T>(a.d, G, xcd, true, append);
   }
   if (!tiled) {
     if (a.d > 64 * kGenericMaxPerLane) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: head_dim > 512");
@@ -969,12 +1102,22 @@ struct PrefixHint {
   int64_t pages, split_len;
 };
 
+struct AppendSource {
+  const void* k_new;
+  const int64_t* k_strides;  // row, head, dim (elements)
+  const void* v_new;
+  const int64_t* v_strides;
+  const int64_t* write_blocks;
+  const int64_t* write_offsets;
+  int64_t n_write;
+};
+
 int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache, const void* value_cache,
                  const int64_t* kv_strides, const int32_t* block_tables, int64_t table_stride, int64_t max_table_width,
                  const int32_t* context_lengths, void* out, const int64_t* out_strides, int64_t n_rows,
                  int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks,
                  float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream,
-                 const PrefixHint* hint) {
+                 const PrefixHint* hint, const AppendSource* append = nullptr) {
   const int esize = dtype_size(dtype);
   if (!esize) return fail(RLT_EINVAL, "rlt_paged_decode: unknown dtype %d", dtype);
   if (n_rows < 0) return fail(RLT_EINVAL, "rlt_paged_decode: n_rows is negative");
@@ -1028,6 +1171,21 @@ int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
     a.prefix_pages = static_cast<int>(hint->pages);
     a.prefix_split_len = static_cast<int>(hint->split_len);
   }
+  if (append) {
+    if (append->n_write < 0 || append->n_write > n_rows)
+      return fail(RLT_EINVAL, "rlt_paged_decode_append: n_write must be in [0, n_rows]");
+    if (append->n_write > 0 && (!append->k_new || !append->v_new || !append->k_strides || !append->v_strides ||
+                                !append->write_blocks || !append->write_offsets))
+      return fail(RLT_EINVAL, "rlt_paged_decode_append: NULL append argument");
+    if (append->n_write > 0) {
+      a.kn_row = append->k_strides[0];
+      a.kn_head = append->k_strides[1];
+      a.kn_dim = append->k_strides[2];
+      a.vn_row = append->v_strides[0];
+      a.vn_head = append->v_strides[1];
+      a.vn_dim = append->v_strides[2];
+    }
+  }
   hipStream_t s = as_stream(stream);
   for (int64_t r0 = 0; r0 < n_rows; r0 += kMaxRowsPerLaunch) {
     const int64_t rows = std::min<int64_t>(kMaxRowsPerLaunch, n_rows - r0);
@@ -1036,6 +1194,14 @@ int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
     a.tables = block_tables + r0 * table_stride;
     a.lens = context_lengths + r0;
     a.n_rows = static_cast<int>(rows);
+    a.n_write = 0;
+    if (append && append->n_write > r0) {
+      a.n_write = static_cast<int>(std::min<int64_t>(rows, append->n_write - r0));
+      a.k_new = static_cast<const char*>(append->k_new) + r0 * a.kn_row * esize;
+      a.v_new = static_cast<const char*>(append->v_new) + r0 * a.vn_row * esize;
+      a.write_blocks = append->write_blocks + r0;
+      a.write_offsets = append->write_offsets + r0;
+    }
     int rc = RLT_OK;
     switch (dtype) {
       case RLT_BFLOAT16: rc = launch_decode<bf16>(a, max_table_width, s); break;
@@ -1148,6 +1314,19 @@ extern "C" int rlt_paged_decode_no_alloc(const void* q, const int64_t* q_strides
     if (rc) return rc;
   }
   return RLT_OK;
+}
+
+extern "C" int rlt_paged_decode_append(
+    const void* q, const int64_t* q_strides, void* key_cache, void* value_cache, const int64_t* kv_strides,
+    const int32_t* block_tables, int64_t table_stride, int64_t max_table_width, const int32_t* context_lengths,
+    void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t page_size, int64_t num_blocks, float scale, int dtype, const void* k_new,
+    const int64_t* k_new_strides, const void* v_new, const int64_t* v_new_strides, const int64_t* write_blocks,
+    const int64_t* write_offsets, int64_t n_write, void* workspace, int64_t workspace_bytes, void* stream) {
+  const AppendSource append{k_new, k_new_strides, v_new, v_new_strides, write_blocks, write_offsets, n_write};
+  return paged_decode(q, q_strides, key_cache, value_cache, kv_strides, block_tables, table_stride, max_table_width,
+                      context_lengths, out, out_strides, n_rows, num_q_heads, num_kv_heads, head_dim, page_size,
+                      num_blocks, scale, dtype, workspace, workspace_bytes, stream, nullptr, &append);
 }
 
 extern "C" int rlt_paged_decode_shared_prefix(

@@ -71,6 +71,12 @@ SIGNATURES = {
         + [c_int64] * 6
         + [c_float, c_int, c_void_p, c_int64, c_void_p],
     ),
+    "rlt_paged_decode_append": (
+        c_int,
+        [c_void_p, _i64p, c_void_p, c_void_p, _i64p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, _i64p]
+        + [c_int64] * 6
+        + [c_float, c_int, c_void_p, _i64p, c_void_p, _i64p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p],
+    ),
     "rlt_paged_decode_no_alloc": (
         c_int,
         [c_void_p, _i64p, c_void_p, c_void_p, _i64p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, _i64p]

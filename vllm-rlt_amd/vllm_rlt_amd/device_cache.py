@@ -12,8 +12,13 @@ from . import ops
 
 
 class DeviceCache:
-    def __init__(self, cache):
+    """fused_append: _write_attend_prepared runs one rlt_paged_decode_append
+    launch (the captured batches' rows are independent) instead of the two
+    steps."""
+
+    def __init__(self, cache, *, fused_append: bool = False):
         self.cache = cache
+        self.fused_append = fused_append
 
     def _write_prepared(self, layer, batch, k, v):
         cache = self.cache
@@ -31,4 +36,14 @@ class DeviceCache:
         return cache.attention(
             q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths,
             shared_prefix=getattr(batch, "shared_prefix", None),
+        )
+
+    def _write_attend_prepared(self, layer, batch, q, k, v):
+        if not self.fused_append:
+            self._write_prepared(layer, batch, k, v)
+            return self._attend_prepared(layer, batch, q)
+        cache = self.cache
+        return cache.attention.decode_append(
+            q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths,
+            k, v, batch.write_blocks, batch.write_offsets,
         )

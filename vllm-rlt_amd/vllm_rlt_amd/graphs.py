@@ -12,9 +12,11 @@ Design:
 * GraphCache holds graphs under any hashable key, each captured once on a
   private stream after warm-up runs, all in one memory pool.  bench.py
   captures its loop-step through the same class.
-* One graph per decode row count.  Replays must give the eager bits, and a
-  model's GEMMs may choose other kernels at other row counts, so batches are
-  never padded up to a shared size.
+* One graph per decode row count (and per whether the batch's rows are
+  independent, when the core's fused append-and-attend is captured).
+  Replays must give the eager bits, and a model's GEMMs may choose other
+  kernels at other row counts, so batches are never padded up to a shared
+  size.
 * A graph reads a StaticBatch: one int64 arena [3, rows] (positions, write
   blocks, write offsets) and one int32 arena (lengths, then the [rows, width]
   tables), loaded from the live batch before each replay.
@@ -126,23 +128,24 @@ class RecurrentGraphs:
         self._last_replay = None  # event after the latest replay (static inputs are reused)
         self.captures = self.replays = self.fallbacks = 0
 
-    def _serves(self, rows: int, batch) -> bool:
-        if not 0 < rows <= self.max_batch_size or batch.cu_seqlens_q is not None:
+    def _serves(self, key, batch) -> bool:
+        if not 0 < key[0] <= self.max_batch_size or batch.cu_seqlens_q is not None:
             return False
-        return rows in self._entries or len(self._entries) < self.max_graphs
+        return key in self._entries or len(self._entries) < self.max_graphs
 
-    def _entry(self, rows: int, hidden: torch.Tensor) -> _Entry:
-        entry = self._entries.get(rows)
+    def _entry(self, key, hidden: torch.Tensor) -> _Entry:
+        entry = self._entries.get(key)
         if entry is None:
+            rows = key[0]
             entry = _Entry(torch.empty_like(hidden[:rows]), StaticBatch(rows, self.width, self.cache.device))
         return entry
 
-    def _capture(self, rows: int, entry: _Entry) -> None:
-        # The warm-up runs grow the attention backend's workspace for `rows`
-        # rows, so the captured kernels see its final address.
-        proxy = DeviceCache(self.cache)
-        entry.graph, entry.output = self.graphs.capture(rows, lambda: self.core(entry.hidden, entry.batch, proxy))
-        self._entries[rows] = entry
+    def _capture(self, key, entry: _Entry) -> None:
+        # The warm-up runs grow the attention backend's workspace for the
+        # graph's rows, so the captured kernels see its final address.
+        proxy = DeviceCache(self.cache, fused_append=key[1])
+        entry.graph, entry.output = self.graphs.capture(key, lambda: self.core(entry.hidden, entry.batch, proxy))
+        self._entries[key] = entry
         self.captures += 1
 
     @staticmethod
@@ -160,7 +163,11 @@ class RecurrentGraphs:
     @torch.inference_mode()
     def run(self, hidden: torch.Tensor, batch):
         rows = len(batch.rows)
-        if not self._serves(rows, batch):
+        # Graphs are keyed by row count and by whether the batch's rows are
+        # independent (then the core's fused append-and-attend is captured).
+        fused = rows > 0 and batch.cu_seqlens_q is None and self.cache._rows_independent(batch)
+        key = (rows, fused)
+        if not self._serves(key, batch):
             self.fallbacks += 1
             return self.core(hidden, self._unpadded(batch, rows), self.cache)
         cache = self.cache
@@ -169,11 +176,11 @@ class RecurrentGraphs:
         stream = torch.cuda.current_stream(cache.device)
         if self._last_replay is not None:
             stream.wait_event(self._last_replay)  # the previous replay still reads the static inputs
-        entry = self._entry(rows, hidden)
+        entry = self._entry(key, hidden)
         entry.hidden.copy_(hidden[:rows])
         entry.batch.load(batch)
         if entry.graph is None:
-            self._capture(rows, entry)
+            self._capture(key, entry)
         entry.graph.replay()
         # The graph's outputs are overwritten by its next replay: hand out copies.
         output = entry.output

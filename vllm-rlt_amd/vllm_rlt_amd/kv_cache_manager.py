@@ -267,6 +267,51 @@ class KVCacheManager(KVPageBook):
             q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths
         )
 
+    def _rows_independent(self, batch: PreparedKVBatch) -> bool:
+        """No row of this decode batch reads a KV slot another row writes.
+
+        Holds when every (request, storage plane) has one row: a row writes
+        only its own plane's private page at its own position, and pages
+        shared between requests (an aliased prefix) are never written.
+        """
+        if batch.cu_seqlens_q is not None:
+            return False
+        planes = {(id(allocation), self._plane(depth)) for allocation, depth, _ in batch.rows}
+        return len(planes) == len(batch.rows)
+
+    @torch.no_grad()
+    def _write_attend_prepared(
+        self, layer: int, batch: PreparedKVBatch, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
+    ) -> torch.Tensor:
+        """_write_prepared then _attend_prepared (:520-586) as one launch where that gives the same bits.
+
+        A decode batch whose rows are independent (_rows_independent) runs
+        rlt_paged_decode_append; any other batch (packed prefill, a request
+        twice on one plane, a shared-prefix hint) runs the two steps.
+        """
+        if not self._rows_independent(batch) or getattr(batch, "shared_prefix", None) is not None:
+            self._write_prepared(layer, batch, k, v)
+            return self._attend_prepared(layer, batch, q)
+        self._validate_layer(layer)
+        self._require_live_batch(batch)
+        if not batch.writable:
+            raise ValueError("a read-only prepared KV batch cannot be written")
+        n = len(batch.position_ids)
+        self._validate_tensor(k, n, "k")
+        self._validate_tensor(v, n, "v")
+        self._validate_tensor(q, n, "q", query=True)
+        if not batch.rows:
+            return torch.empty_like(q)
+        # Each row's history before its new token must already be there.
+        for allocation, depth, position in batch.rows:
+            self._require_prefix(allocation, layer, depth, position)
+        out = self.attention.decode_append(
+            q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths,
+            k, v, batch.write_blocks, batch.write_offsets, n_write=len(batch.rows),
+        )
+        self._record_written(batch, layer)
+        return out
+
     @torch.no_grad()
     def finalize_token(self, request_id: str, position: int, exit_depth: int) -> None:
         """Copy the exit depth's K/V of one token into every unexecuted depth (:588-614)."""

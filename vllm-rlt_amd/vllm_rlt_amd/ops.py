@@ -352,24 +352,8 @@ def shared_prefix(rows, pages, n_rows: int, lengths, device) -> SharedPrefix:
     )
 
 
-def paged_decode(
-    q: torch.Tensor,
-    key_cache: torch.Tensor,
-    value_cache: torch.Tensor,
-    block_tables: torch.Tensor,
-    context_lengths: torch.Tensor,
-    out: torch.Tensor | None = None,
-    workspace: torch.Tensor | None = None,
-    scale: float | None = None,
-    shared_prefix: SharedPrefix | None = None,
-) -> torch.Tensor:
-    """Paged decode attention over layer-slice caches [blocks, page, kv_heads, head_dim].
-
-    Same contract as torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36):
-    returns a new tensor like q unless out is given.  With `shared_prefix` the
-    listed rows' common prefix pages are read once for all of them
-    (rlt_paged_decode_shared_prefix); the result is the same attention.
-    """
+def _decode_inputs(q, key_cache, value_cache, block_tables, context_lengths, out):
+    """Validated decode geometry: (device, rows, hq, hkv, d, page, num_blocks, out)."""
     device = _require_rocm(q, key_cache, value_cache, block_tables, context_lengths)
     if q.ndim != 3 or key_cache.ndim != 4:
         raise ValueError("q must be [rows, heads, head_dim] and caches [blocks, page, kv_heads, head_dim]")
@@ -392,13 +376,88 @@ def paged_decode(
         out = torch.empty_like(q)
     elif out.shape != q.shape or out.dtype != q.dtype or out.device != device:
         raise ValueError("out must match q")
-    if rows == 0:
-        return out
+    return device, rows, hq, hkv, d, page, nb, out
+
+
+def _decode_workspace(workspace, rows, hq, hkv, d, device):
     need = decode_workspace_bytes(rows, hq, hkv, d)
     if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=device)
-    elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
+        return torch.empty(need, dtype=torch.uint8, device=device)
+    if workspace.numel() * workspace.element_size() < need or workspace.device != device:
         raise ValueError(f"workspace must hold {need} bytes on {device}")
+    return workspace
+
+
+def paged_decode_append(
+    q: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lengths: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    write_blocks: torch.Tensor,
+    write_offsets: torch.Tensor,
+    n_write: int | None = None,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """KV append of rows [0, n_write) then decode attention, in one launch (rlt_paged_decode_append).
+
+    key_cache / value_cache are layer slices [blocks, page, kv_heads, head_dim]
+    and are written.  Same pages and output bits as kv_append followed by
+    paged_decode, provided no row reads a slot another row writes (a decode
+    batch with one row per request and depth).
+    """
+    device, rows, hq, hkv, d, page, nb, out = _decode_inputs(q, key_cache, value_cache, block_tables, context_lengths, out)
+    _require_rocm(q, k_new, v_new, write_blocks, write_offsets)
+    n = write_blocks.shape[0] if n_write is None else int(n_write)
+    for t, name in ((k_new, "k_new"), (v_new, "v_new")):
+        if t.ndim != 3 or t.shape[1:] != (hkv, d) or t.shape[0] < n or t.dtype != key_cache.dtype:
+            raise ValueError(f"{name} must be [>= n_write, {hkv}, {d}] {key_cache.dtype}")
+    _require_int(write_blocks, torch.int64, "write_blocks")
+    _require_int(write_offsets, torch.int64, "write_offsets")
+    if not 0 <= n <= min(rows, write_blocks.shape[0], write_offsets.shape[0]):
+        raise ValueError("n_write must be in [0, rows] and covered by write_blocks / write_offsets")
+    if rows == 0:
+        return out
+    workspace = _decode_workspace(workspace, rows, hq, hkv, d, device)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    rc = _native.load().rlt_paged_decode_append(
+        q.data_ptr(), int64_array(q.stride()), key_cache.data_ptr(), value_cache.data_ptr(),
+        int64_array(key_cache.stride()), block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        context_lengths.data_ptr(), out.data_ptr(), int64_array(out.stride()), rows, hq, hkv, d, page, nb, scale,
+        dtype_code(q.dtype), k_new.data_ptr(), int64_array(k_new.stride()), v_new.data_ptr(),
+        int64_array(v_new.stride()), write_blocks.data_ptr(), write_offsets.data_ptr(), n, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), stream_handle(device),
+    )
+    check(rc, "rlt_paged_decode_append")
+    return out
+
+
+def paged_decode(
+    q: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lengths: torch.Tensor,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    scale: float | None = None,
+    shared_prefix: SharedPrefix | None = None,
+) -> torch.Tensor:
+    """Paged decode attention over layer-slice caches [blocks, page, kv_heads, head_dim].
+
+    Same contract as torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36):
+    returns a new tensor like q unless out is given.  With `shared_prefix` the
+    listed rows' common prefix pages are read once for all of them
+    (rlt_paged_decode_shared_prefix); the result is the same attention.
+    """
+    device, rows, hq, hkv, d, page, nb, out = _decode_inputs(q, key_cache, value_cache, block_tables, context_lengths, out)
+    if rows == 0:
+        return out
+    workspace = _decode_workspace(workspace, rows, hq, hkv, d, device)
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     if shared_prefix is not None and rows > DECODE_SHARED_PREFIX_MAX_ROWS:
         shared_prefix = None  # an optimisation only: larger batches read the prefix per row

@@ -97,6 +97,18 @@ class HipPagedAttention:
             q, key_cache, value_cache, block_tables, context_lengths, workspace=workspace, shared_prefix=shared_prefix
         )
 
+    def decode_append(self, q, key_cache, value_cache, block_tables, context_lengths, k_new, v_new, write_blocks,
+                      write_offsets, n_write=None):
+        """Append rows' new K/V, then decode attention, in one launch (beyond the reference's interface).
+
+        The caller guarantees that no row reads a slot another row writes.
+        """
+        workspace = self.reserve_decode(q.shape[0], q.shape[1], key_cache.shape[2]) if q.shape[0] else None
+        return ops.paged_decode_append(
+            q, key_cache, value_cache, block_tables, context_lengths, k_new, v_new, write_blocks, write_offsets,
+            n_write=n_write, workspace=workspace,
+        )
+
     def prefill(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q, max_seqlen_q):
         """Packed ragged chunks over paged prefixes, bottom-right causal.
 
