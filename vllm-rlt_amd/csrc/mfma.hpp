@@ -38,6 +38,12 @@ template <> struct MfmaOps<bf16> {
     const bf16x2 r = {static_cast<__bf16>(x), static_cast<__bf16>(y)};  // v_cvt_pk_bf16_f32, RNE
     return __builtin_bit_cast(uint32_t, r);
   }
+  // acc + lo + hi of a packed pair, exactly the rounded values the MFMA reads
+  // (v_dot2c_f32_bf16 against ones).
+  __device__ static float sum2(uint32_t pair, float acc) {
+    const bf16x2 one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, acc, false);
+  }
 };
 template <> struct MfmaOps<f16> {
   using V8 = f16x8;
@@ -45,6 +51,10 @@ template <> struct MfmaOps<f16> {
   __device__ static uint32_t pack2(float x, float y) {
     const f16x2 r = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
     return __builtin_bit_cast(uint32_t, r);
+  }
+  __device__ static float sum2(uint32_t pair, float acc) {
+    const f16x2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), one, acc, false);
   }
 };
 

@@ -587,36 +587,45 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// The fused append's page write of row r's kv head h: 16-byte chunks of the
-// [D] slab from k_new / v_new to (write_blocks[r], write_offsets[r]).  A slot
-// outside the pool is skipped.
-template <typename T, int D>
-__device__ __forceinline__ void store_new_token(const DecodeArgs& a, int r, int h, int lane) {
-  constexpr int kChunks = D * static_cast<int>(sizeof(T)) / 16;
-  static_assert(kChunks <= 64, "one lane per 16-byte chunk");
-  const int64_t b = a.write_blocks[r], o = a.write_offsets[r];
-  if (b < 0 || b >= a.num_blocks || o < 0 || o >= a.page || lane >= kChunks) return;
-  const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head;
-  const T* kn = static_cast<const T*>(a.k_new) + r * a.kn_row + static_cast<int64_t>(h) * a.kn_head;
-  const T* vn = static_cast<const T*>(a.v_new) + r * a.vn_row + static_cast<int64_t>(h) * a.vn_head;
-  reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.k) + slot))[lane] =
-      reinterpret_cast<const u32x4*>(kn)[lane];
-  reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.v) + slot))[lane] =
-      reinterpret_cast<const u32x4*>(vn)[lane];
-}
-
 // Merge kernel: one wavefront per (row, kv_head) with more than one split;
-// with a fused append also the page write of every appending (row, kv_head).
+// with a fused append also the page write of every appending (row, kv_head):
+// 16-byte chunks of the [D] slab from k_new / v_new to (write_blocks[r],
+// write_offsets[r]), skipped when the slot is outside the pool.  Every load
+// that does not depend on the row's split count (its length, the write slot,
+// the new token) goes out together, and the token is stored last: a store
+// ahead of the partial loads would hold them back, since the compiler cannot
+// tell the pool from the workspace.  Two memory round trips in all.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
+  constexpr int kChunks = D * static_cast<int>(sizeof(T)) / 16;
+  static_assert(kChunks <= 64, "one lane per 16-byte chunk");
   const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (item >= a.n_rows * a.hkv) return;
   const int r = item / a.hkv;
   const int h = item - r * a.hkv;
-  if (r < a.n_write) store_new_token<T, D>(a, r, h, threadIdx.x & 63);
+  const int lane = threadIdx.x & 63;
+  const int len = row_length(a, r);
+  const bool writes = r < a.n_write;
+  int64_t b = -1, o = -1;
+  u32x4 kt = {}, vt = {};
+  if (writes) {
+    b = a.write_blocks[r];
+    o = a.write_offsets[r];
+    if (lane < kChunks) {
+      kt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + r * a.kn_row +
+                                          static_cast<int64_t>(h) * a.kn_head)[lane];
+      vt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + r * a.vn_row +
+                                          static_cast<int64_t>(h) * a.vn_head)[lane];
+    }
+  }
   int split_len, ns;
-  split_plan(row_length(a, r), &split_len, &ns);
-  if (ns > 1) merge_partials<T, D>(a, r, h, ns, threadIdx.x & 63);
+  split_plan(len, &split_len, &ns);
+  if (ns > 1) merge_partials<T, D>(a, r, h, ns, lane);
+  if (writes && b >= 0 && b < a.num_blocks && o >= 0 && o < a.page && lane < kChunks) {
+    const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head;
+    reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.k) + slot))[lane] = kt;
+    reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.v) + slot))[lane] = vt;
+  }
 }
 
 // Shared-prefix pass: the split partials of the splits that prefix_takes()

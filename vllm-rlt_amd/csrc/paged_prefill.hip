@@ -415,12 +415,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
   for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
   float m = -INFINITY;
-  // Row sums of P, accumulated by MFMA against a ones operand: every element
-  // of lane l holds the sum for query column l % 32 (over the rounded P that
-  // also weights V), so the softmax phase spends no vector adds on it.
-  f32x16 acc_l = {};
-  const uint32_t one2 = Ops::pack2(1.f, 1.f);
-  const u32x4 ones = {one2, one2, one2, one2};
+  // This lane's share of its query's row sum: the keys it holds, summed from
+  // the rounded P that also weights V (v_dot2 against ones, in the softmax
+  // phase; the lane 32 away holds the other keys).
+  float lsum = 0.f;
 
   // Whether the wave computes tile j: it exists and holds a key visible to
   // one of the wave's queries.  Once false it stays false for later tiles.
@@ -447,8 +445,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // rows only), tile maximum, exponentials.  Leaves P^T rounded to T as the B
   // operands of the four 16-key k-steps.  Element r of half hh holds key
   // key0 + 32hh + 8(r/4) + 4half + r%4.  When the running maximum moves it
-  // returns true with the accumulators' factor in corr; accumulate() applies
-  // it, so acc_o and acc_l change in one place only.  hook(0) .. hook(7) run
+  // returns true with the accumulators' factor in corr, which the row sum takes
+  // here and acc_o in accumulate().  hook(0) .. hook(7) run
   // at fixed points along the way (the staging loads of the direct-to-LDS
   // path, spread out so that they never queue up behind one another).
   auto softmax = [&](int key0, f32x16 (&sacc)[2], u32x4 (&pb)[4], float& corr, auto&& hook)
@@ -478,6 +476,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       const float mn = fmaxf(m, tmax);
       corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
       m = mn;
+      lsum *= corr;
     }
     hook(2);
     // p = 2^(s * scale * log2(e) - m); a lane that has seen no key yet has
@@ -498,18 +497,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         pb[ks][e] = Ops::pack2(sacc[ks / 2][(ks % 2) * 8 + 2 * e], sacc[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lsum = Ops::sum2(pb[ks][e], lsum);
     return rescale;
   };
   // O^T = O^T * corr (when softmax() moved the maximum) + V^T P^T over the
-  // tile's four 16-key k-steps; the row sums likewise.
+  // tile's four 16-key k-steps.
   auto accumulate = [&](int b, const u32x4 (&pb)[4], bool rescale, float corr) __attribute__((always_inline)) {
     if (rescale) {
 #pragma unroll
       for (int c = 0; c < DTILES; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_l[r] *= corr;
     }
     const uint16_t* v_lds = group_lds + b * (KT + VT) + KT;
     const int key = DMA ? opaque(v_key) : 0;
@@ -528,7 +529,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
         acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb[ks]), acc_o[c]);
       }
-      acc_l = Ops::mma(as_v8<V8>(ones), as_v8<V8>(pb[ks]), acc_l);
     }
   };
   const int niter = (ntiles + 1) / 2;  // tiles per key group (the last of group 1 may not exist)
@@ -659,7 +659,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   float* xs = reinterpret_cast<float*>(lds) + qw * MERGE_FLOATS * 64 + lane;
   if (kg == 1) {
     xs[0] = m;
-    xs[64] = acc_l[0];
+    xs[64] = lsum;
 #pragma unroll
     for (int c = 0; c < DTILES; ++c)
 #pragma unroll
@@ -673,7 +673,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const float mm = fmaxf(m, m1);
     const float c0 = (m == -INFINITY) ? 0.f : fast_exp2(m - mm);
     const float c1 = (m1 == -INFINITY) ? 0.f : fast_exp2(m1 - mm);
-    total = acc_l[0] * c0 + xs[64] * c1;
+    total = lsum * c0 + xs[64] * c1;
+    total += __shfl_xor(total, 32, 64);  // the two halves hold the row's two key halves
 #pragma unroll
     for (int c = 0; c < DTILES; ++c)
 #pragma unroll
