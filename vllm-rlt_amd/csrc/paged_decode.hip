@@ -79,24 +79,19 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
 constexpr float kLog2e = 1.4426950408889634f;
 
 __host__ __device__ inline void split_plan(int len, int* split_len, int* nsplit) {
-  if (len <= 0) {  // one item that writes the all-zero row
-    *split_len = kSplitTokens;
-    *nsplit = 1;
-    return;
-  }
-  const int n = (len + kSplitTokens - 1) / kSplitTokens;
-  if (n <= kMaxSplits) {
-    *split_len = kSplitTokens;
-    *nsplit = n;
-    return;
-  }
-  // Longer rows double the split length until kMaxSplits cover the row, so
-  // rows of similar length cut their contexts at the same token offsets (an
-  // aliased prefix then falls into the same splits of every row).
-  int per = kSplitTokens;
-  while ((len + per - 1) / per > kMaxSplits) per <<= 1;
+  // Rows longer than kMaxSplits splits double the split length until
+  // kMaxSplits cover the row, so rows of similar length cut their contexts at
+  // the same token offsets (an aliased prefix then falls into the same splits
+  // of every row).  The doubling count is the smallest k >= 0 with
+  // kMaxSplits * (kSplitTokens << k) >= len, taken from a leading-zero count
+  // so the plan has no loop (the merge kernel issues its loads around it).
+  // An empty row is one item that writes the all-zero row.
+  constexpr unsigned kCover = static_cast<unsigned>(kMaxSplits) * kSplitTokens;
+  const unsigned m = len > 0 ? (static_cast<unsigned>(len) + kCover - 1) / kCover : 1u;
+  const int k = m <= 1 ? 0 : 32 - __builtin_clz(m - 1);
+  const int per = kSplitTokens << k;
   *split_len = per;
-  *nsplit = (len + per - 1) / per;
+  *nsplit = len > 0 ? (len + per - 1) / per : 1;
 }
 
 struct DecodeArgs {
@@ -222,60 +217,87 @@ __device__ __forceinline__ int find_row(const int* prefix, int n, int x) {
   return lo;
 }
 
-// Merges the ns >= 2 split partials of (row r, kv head h) into the output.
-// Lane sp holds split sp's (max, sum) (kMaxSplits == 64 == wave size), so the
-// global max and the normaliser are two wave reductions; lane l sums dims
-// l, l + 64, ... over splits in split order.  The accumulator loads do not
-// depend on the reductions, so the first batch (all of the lane's dims for up
-// to 64 / (D / 64) splits) is issued together with the (max, sum) load: one
-// round trip to memory for the common split counts instead of one per eight
-// splits.  The result depends only on the row's own partials.
-template <typename T, int D>
-__device__ void merge_partials(const DecodeArgs& a, int r, int h, int ns, int lane) {
-  static_assert(kMaxSplits == 64, "one lane per split");
-  static_assert(D % 64 == 0 && D <= 256, "dims per lane");
-  constexpr int DPL = D / 64;      // dims per lane
-  constexpr int SPB = 64 / DPL;    // splits per load batch
+// Merges the split partials of (row r, kv head h) into the output when the
+// row has ns >= 2 splits.  Lane sp holds split sp's (max, sum) (kMaxSplits ==
+// 64 == wave size), so the global max and the normaliser are two wave
+// reductions; lane l sums dims l, l + 64, ... over splits in split order.  The
+// (max, sum) of all 64 slots and the first batch of accumulators (all of the
+// lane's dims for up to 64 / (D / 64) splits) are loaded whatever ns is --
+// every slot lies inside the workspace -- and the slots past ns are selected
+// away afterwards, so none of these loads waits for the row's length: the
+// merge costs one round trip to memory for the common split counts.  The
+// result depends only on the row's own partials.
+template <int D>
+struct MergeLoads {
+  static constexpr int DPL = D / 64;    // dims per lane
+  static constexpr int SPB = 64 / DPL;  // splits per load batch
+  float2 ml;                            // this lane's split's (max, sum)
+  float x[DPL][SPB];                    // the first batch of accumulators
+};
+
+// The (max, sum) of all 64 split slots of (row r, kv head h, query j) and the
+// first batch of accumulators: every slot lies inside the workspace, so they
+// load whatever the row's split count is.
+template <int D>
+__device__ __forceinline__ MergeLoads<D> load_partials(const DecodeArgs& a, int r, int h, int j, int lane) {
+  using L = MergeLoads<D>;
   const int G = a.hq / a.hkv;
   const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
   const int64_t split_stride = static_cast<int64_t>(G) * D;
-  for (int j = 0; j < G; ++j) {
-    T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
-    const float* base = a.ws_acc + (slot0 * G + j) * D + lane;
-    const float2 ml = lane < ns ? a.ws_ml[(slot0 + lane) * G + j] : make_float2(-INFINITY, 0.f);
+  const float* base = a.ws_acc + (slot0 * G + j) * D + lane;
+  L v;
+  v.ml = a.ws_ml[(slot0 + lane) * G + j];
+#pragma unroll
+  for (int u = 0; u < L::SPB; ++u)
+#pragma unroll
+    for (int dd = 0; dd < L::DPL; ++dd) v.x[dd][u] = base[u * split_stride + dd * 64];
+  return v;
+}
+
+template <typename T, int D>
+__device__ void merge_partials(const DecodeArgs& a, int r, int h, int j, int ns, int lane, MergeLoads<D> v) {
+  // ns < 2: nothing to merge (the split pass wrote the row); only the store is skipped, so the
+  // loads of v stay unconditional.
+  const bool live = ns > 1;
+  static_assert(kMaxSplits == 64, "one lane per split");
+  static_assert(D % 64 == 0 && D <= 256, "dims per lane");
+  constexpr int DPL = MergeLoads<D>::DPL;
+  constexpr int SPB = MergeLoads<D>::SPB;
+  const int G = a.hq / a.hkv;
+  const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
+  const int64_t split_stride = static_cast<int64_t>(G) * D;
+  T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
+  const float* base = a.ws_acc + (slot0 * G + j) * D + lane;
+  const float2 ml = lane < ns ? v.ml : make_float2(-INFINITY, 0.f);
+  const float M = strided_max<1>(ml.x);
+  const float w = lane < ns ? fast_exp2(ml.x - M) : 0.f;
+  const float inv = 1.f / group_sum<64>(ml.y * w);
+  float acc[DPL];
+#pragma unroll
+  for (int dd = 0; dd < DPL; ++dd) acc[dd] = 0.f;
+#pragma unroll
+  for (int u = 0; u < SPB; ++u) {
+    const float wu = __shfl(w, u, 64);
+#pragma unroll
+    for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(u < ns ? v.x[dd][u] : 0.f, wu, acc[dd]);
+  }
+  // Further splits (long rows), a whole batch of loads in flight at a time.
+  for (int sp0 = SPB; live && sp0 < ns; sp0 += SPB) {
     float x[DPL][SPB];
 #pragma unroll
     for (int u = 0; u < SPB; ++u)
 #pragma unroll
-      for (int dd = 0; dd < DPL; ++dd) x[dd][u] = u < ns ? base[u * split_stride + dd * 64] : 0.f;
-    const float M = strided_max<1>(ml.x);
-    const float w = lane < ns ? fast_exp2(ml.x - M) : 0.f;
-    const float inv = 1.f / group_sum<64>(ml.y * w);
-    float acc[DPL];
-#pragma unroll
-    for (int dd = 0; dd < DPL; ++dd) acc[dd] = 0.f;
+      for (int dd = 0; dd < DPL; ++dd) x[dd][u] = sp0 + u < ns ? base[(sp0 + u) * split_stride + dd * 64] : 0.f;
 #pragma unroll
     for (int u = 0; u < SPB; ++u) {
-      const float wu = __shfl(w, u, 64);
+      const float wu = __shfl(w, (sp0 + u) & 63, 64);
 #pragma unroll
       for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(x[dd][u], wu, acc[dd]);
     }
-    // Further splits (long rows), a whole batch of loads in flight at a time.
-    for (int sp0 = SPB; sp0 < ns; sp0 += SPB) {
-#pragma unroll
-      for (int u = 0; u < SPB; ++u)
-#pragma unroll
-        for (int dd = 0; dd < DPL; ++dd) x[dd][u] = sp0 + u < ns ? base[(sp0 + u) * split_stride + dd * 64] : 0.f;
-#pragma unroll
-      for (int u = 0; u < SPB; ++u) {
-        const float wu = __shfl(w, (sp0 + u) & 63, 64);
-#pragma unroll
-        for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(x[dd][u], wu, acc[dd]);
-      }
-    }
-#pragma unroll
-    for (int dd = 0; dd < DPL; ++dd) store_elem(orow + (lane + dd * 64) * a.o_dim, acc[dd] * inv);
   }
+#pragma unroll
+  for (int dd = 0; dd < DPL; ++dd)
+    if (live) store_elem(orow + (lane + dd * 64) * a.o_dim, acc[dd] * inv);
 }
 
 template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX, bool APPEND>
@@ -588,40 +610,44 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 }
 
 // Merge kernel: one wavefront per (row, kv_head) with more than one split;
-// with a fused append also the page write of every appending (row, kv_head):
-// 16-byte chunks of the [D] slab from k_new / v_new to (write_blocks[r],
-// write_offsets[r]), skipped when the slot is outside the pool.  Every load
-// that does not depend on the row's split count (its length, the write slot,
-// the new token) goes out together, and the token is stored last: a store
-// ahead of the partial loads would hold them back, since the compiler cannot
-// tell the pool from the workspace.  Two memory round trips in all.
-template <typename T, int D>
+// with a fused append (APPEND) also the page write of every appending (row,
+// kv_head): 16-byte chunks of the [D] slab from k_new / v_new to
+// (write_blocks[r], write_offsets[r]), skipped when the slot is outside the
+// pool.  All loads go out before the first wait: the row's length, the write
+// slot and the new token (read from a clamped row and chunk, so no load needs
+// a branch) and the partials (merge_partials).  The token is stored last: a
+// store ahead of the partial loads would hold them back, since the compiler
+// cannot tell the pool from the workspace.
+template <typename T, int D, bool APPEND>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int kChunks = D * static_cast<int>(sizeof(T)) / 16;
-  static_assert(kChunks <= 64, "one lane per 16-byte chunk");
+  static_assert(kChunks <= 64 && 64 % kChunks == 0, "whole chunks per lane group");
   const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (item >= a.n_rows * a.hkv) return;
   const int r = item / a.hkv;
   const int h = item - r * a.hkv;
   const int lane = threadIdx.x & 63;
   const int len = row_length(a, r);
-  const bool writes = r < a.n_write;
   int64_t b = -1, o = -1;
   u32x4 kt = {}, vt = {};
-  if (writes) {
-    b = a.write_blocks[r];
-    o = a.write_offsets[r];
-    if (lane < kChunks) {
-      kt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + r * a.kn_row +
-                                          static_cast<int64_t>(h) * a.kn_head)[lane];
-      vt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + r * a.vn_row +
-                                          static_cast<int64_t>(h) * a.vn_head)[lane];
-    }
+  if constexpr (APPEND) {  // a.n_write >= 1
+    const int rw = min(r, a.n_write - 1);
+    const int chunk = lane % kChunks;
+    b = a.write_blocks[rw];
+    o = a.write_offsets[rw];
+    kt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + rw * a.kn_row +
+                                        static_cast<int64_t>(h) * a.kn_head)[chunk];
+    vt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + rw * a.vn_row +
+                                        static_cast<int64_t>(h) * a.vn_head)[chunk];
   }
+  const MergeLoads<D> first = load_partials<D>(a, r, h, 0, lane);
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
   int split_len, ns;
   split_plan(len, &split_len, &ns);
-  if (ns > 1) merge_partials<T, D>(a, r, h, ns, lane);
-  if (writes && b >= 0 && b < a.num_blocks && o >= 0 && o < a.page && lane < kChunks) {
+  merge_partials<T, D>(a, r, h, 0, ns, lane, first);
+  if (ns > 1)
+    for (int j = 1; j < a.hq / a.hkv; ++j) merge_partials<T, D>(a, r, h, j, ns, lane, load_partials<D>(a, r, h, j, lane));
+  if (APPEND && r < a.n_write && lane < kChunks && b >= 0 && b < a.num_blocks && o >= 0 && o < a.page) {
     const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head;
     reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.k) + slot))[lane] = kt;
     reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.v) + slot))[lane] = vt;
@@ -1064,9 +1090,15 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   if (int rc = check_launch("rlt_paged_decode")) return rc;
   const int merge_grid = (a.n_rows * a.hkv + kWaves - 1) / kWaves;
   const dim3 mgrid(merge_grid), mblock(64 * kWaves);
-  if (a.d == 64) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 64>), mgrid, mblock, 0, stream, a);
-  else if (a.d == 128) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 128>), mgrid, mblock, 0, stream, a);
-  else hipLaunchKernelGGL((paged_decode_merge_kernel<T, 256>), mgrid, mblock, 0, stream, a);
+  if (append) {
+    if (a.d == 64) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 64, true>), mgrid, mblock, 0, stream, a);
+    else if (a.d == 128) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 128, true>), mgrid, mblock, 0, stream, a);
+    else hipLaunchKernelGGL((paged_decode_merge_kernel<T, 256, true>), mgrid, mblock, 0, stream, a);
+  } else {
+    if (a.d == 64) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 64, false>), mgrid, mblock, 0, stream, a);
+    else if (a.d == 128) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 128, false>), mgrid, mblock, 0, stream, a);
+    else hipLaunchKernelGGL((paged_decode_merge_kernel<T, 256, false>), mgrid, mblock, 0, stream, a);
+  }
   return check_launch("rlt_paged_decode(merge)");
 }
 
