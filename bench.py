@@ -104,20 +104,38 @@ def calibrate_counters(device):
     print(json.dumps({"calibration_copy_bytes": src.numel()}), flush=True)
 
 
+def _profile_figure(key, workload):
+    """The number on a committed profile summary line `<key>[<workload>] = <number>`, if any."""
+    import re
+
+    pattern = re.compile(rf"{re.escape(key)}\[{re.escape(workload)}\]\s*=\s*([0-9.eE+]+)")
+    for path in sorted((REPO / "profiles").glob("*.md")):
+        match = pattern.search(path.read_text())
+        if match:
+            return float(match.group(1))
+    return None
+
+
 def profiled_traffic(workload):
     """HBM bytes per launch of the workload's kernel from the committed rocprofv3 --pmc summary, if any.
 
     The summary carries a line `traffic_bytes_per_launch[<workload>] = <bytes>`
     computed from FETCH_SIZE and WRITE_SIZE scaled by the calibration copy.
     """
-    import re
+    value = _profile_figure("traffic_bytes_per_launch", workload)
+    return None if value is None else int(value)
 
-    pattern = re.compile(rf"traffic_bytes_per_launch\[{re.escape(workload)}\]\s*=\s*(\d+)")
-    for path in sorted((REPO / "profiles").glob("*.md")):
-        match = pattern.search(path.read_text())
-        if match:
-            return int(match.group(1))
-    return None
+
+def profiled_launch_ms(workload):
+    """The launch's average kernel time (ms) in the committed rocprofv3 --kernel-trace summary, if any.
+
+    The summary carries `rocprof_avg_launch_us[<workload>] = <us>`: the traced
+    average of the kernels one launch runs (for the decode, split pass plus
+    merge), reported beside the live HIP-event average, which also holds the
+    gap between those kernels.
+    """
+    value = _profile_figure("rocprof_avg_launch_us", workload)
+    return None if value is None else round(value / 1e3, 5)
 
 
 def describe(name):
@@ -727,6 +745,7 @@ def run_prefill(args, device):
             "unit": "TFLOP/s",
             "frac": round(launch_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": profiled_traffic("ouro-prefill"),
+            "rocprof_avg_launch_ms": profiled_launch_ms("ouro-prefill"),
             "avg_launch_ms": round(launch_ms, 5),
             "median_launch_ms": round(statistics.median(launch_list), 5),
             "launch_ms_iqr": iqr(launch_list),
@@ -908,6 +927,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(args.workload),
+            "rocprof_avg_launch_ms": profiled_launch_ms(args.workload),
             "avg_launch_ms": round(decode_ms, 5),
             "median_launch_ms": round(statistics.median(launch_ms), 5),
             "launch_ms_iqr": iqr(launch_ms),
