@@ -91,6 +91,26 @@ def test_fused_append_equals_two_steps_and_the_oracle(dtype, hq, hkv, d):
     check_against_oracle(case, k_new, v_new, blocks, offsets, n, *got)
 
 
+def test_fused_append_with_a_stale_workspace():
+    # The merge kernel reads the new token from a clamped row and every split slot
+    # before it knows the row's split count; a NaN-filled workspace (what earlier
+    # launches leave) and pad rows past n_write must still give the two-step bits.
+    from vllm_rlt_amd import ops
+
+    case, k_new, v_new, blocks, offsets, n = decode_batch(LENGTHS, hq=16, hkv=16, d=128, dtype=torch.bfloat16,
+                                                          seed=404, n_write=len(LENGTHS) - 3)
+    ref = two_step(case, k_new, v_new, blocks, offsets, n)
+    dev = case.to("cuda")
+    nbytes = ops.decode_workspace_bytes(len(LENGTHS), 16, 16, 128)
+    workspace = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    out = ops.paged_decode_append(dev.q, dev.key_slice, dev.value_slice, dev.tables, dev.lengths, k_new.cuda(),
+                                  v_new.cuda(), blocks.cuda(), offsets.cuda(), n_write=n, workspace=workspace)
+    torch.cuda.synchronize()
+    got = (out.cpu(), dev.key_pool.cpu(), dev.value_pool.cpu())
+    for a, b in zip(got, ref):
+        assert torch.equal(bits(a), bits(b))
+
+
 def test_fused_append_pad_rows_and_empty_rows():
     # Rows past n_write are padding (no write; length 0 reads nothing), and an
     # empty row inside the written range attends to nothing.

@@ -87,6 +87,21 @@ def test_poisoned_slots_never_reach_the_output():
         assert_close(run_hip(case), case)
 
 
+def test_stale_workspace_slots_never_reach_the_output():
+    # The merge loads every split slot of a (row, head) before it knows the row's
+    # split count and discards the slots past it: a workspace full of NaN from
+    # earlier launches must not leak into rows of 1, 2 or 5 splits, or 33+.
+    from vllm_rlt_amd import ops
+
+    lengths = [1, 200, 256, 257, 300, 1029, 0, 8449, 40]
+    case = random_decode_case(lengths, hq=8, hkv=4, d=128, dtype=torch.bfloat16, seed=77).to("cuda")
+    nbytes = ops.decode_workspace_bytes(len(lengths), 8, 4, 128)
+    workspace = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")  # every float slot is NaN
+    out = ops.paged_decode(case.q, case.key_slice, case.value_slice, case.tables, case.lengths, workspace=workspace)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), case.to("cpu"))
+
+
 def test_rows_are_batch_invariant():
     # tests/test_flash_attention.py:193-208: a row's bits do not depend on the batch around it.
     from vllm_rlt_amd import ops
