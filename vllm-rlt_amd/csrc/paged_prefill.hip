@@ -429,27 +429,54 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const uint16_t* k_lds = group_lds + b * (KT + VT);
     const int key = DMA ? opaque(k_key) : 0;
     f32x16 c[2] = {{}, {}};
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
+    if constexpr (DMA) {
+      // The K reads run kAhead k-steps ahead of their MFMAs, pinned in that
+      // order: an LDS read takes longer than the two MFMAs of one k-step, so
+      // reads issued one step ahead leave every step waiting for its operand.
+      constexpr int kAhead = 3;
+      auto rd = [&](int ks, int hh) __attribute__((always_inline)) {
         const char* row = reinterpret_cast<const char*>(k_lds + hh * 32 * KROW);
-        const u32x4 kv = DMA ? *reinterpret_cast<const u32x4*>(row + (((ks << 5) ^ key) + k_base))
-                             : *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
-        c[hh] = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c[hh]);
+        return *reinterpret_cast<const u32x4*>(row + (((ks << 5) ^ key) + k_base));
+      };
+      u32x4 kq[kAhead + 1][2];
+#pragma unroll
+      for (int ks = 0; ks < kAhead; ++ks)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) kq[ks][hh] = rd(ks, hh);
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        if (ks + kAhead < KSTEPS)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) kq[(ks + kAhead) % (kAhead + 1)][hh] = rd(ks + kAhead, hh);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          c[hh] = Ops::mma(as_v8<V8>(kq[ks % (kAhead + 1)][hh]), as_v8<V8>(qb[ks]), c[hh]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
+          c[hh] = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c[hh]);
+        }
+    }
     sacc[0] = c[0];
     sacc[1] = c[1];
   };
   // Online softmax of tile key0: mask (diagonal tiles and the chunk's last
-  // rows only), tile maximum, exponentials.  Leaves P^T rounded to T as the B
-  // operands of the four 16-key k-steps.  Element r of half hh holds key
+  // rows only), tile maximum, exponentials.  Leaves P^T in fp32 in sacc;
+  // accumulate() rounds it to T one 16-key k-step at a time, next to that
+  // step's MFMAs, where the VALU work hides under them instead of lengthening
+  // this phase.  Element r of half hh holds key
   // key0 + 32hh + 8(r/4) + 4half + r%4.  When the running maximum moves it
   // returns true with the accumulators' factor in corr, which the row sum takes
   // here and acc_o in accumulate().  hook(0) .. hook(7) run
   // at fixed points along the way (the staging loads of the direct-to-LDS
   // path, spread out so that they never queue up behind one another).
-  auto softmax = [&](int key0, f32x16 (&sacc)[2], u32x4 (&pb)[4], float& corr, auto&& hook)
+  auto softmax = [&](int key0, f32x16 (&sacc)[2], float& corr, auto&& hook)
                      __attribute__((always_inline)) -> bool {
     float tmax = -INFINITY;
     if (uniform(key0 + kBN - 1 > prefix + wave_row0 || wave_row0 + 31 >= nq)) {
@@ -492,20 +519,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
       if (hh == 0) hook(5);
     }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        pb[ks][e] = Ops::pack2(sacc[ks / 2][(ks % 2) * 8 + 2 * e], sacc[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lsum = Ops::sum2(pb[ks][e], lsum);
     return rescale;
   };
   // O^T = O^T * corr (when softmax() moved the maximum) + V^T P^T over the
-  // tile's four 16-key k-steps.
-  auto accumulate = [&](int b, const u32x4 (&pb)[4], bool rescale, float corr) __attribute__((always_inline)) {
+  // tile's four 16-key k-steps.  Each step packs its P^T operand to T and
+  // adds exactly those rounded values to the row sum (v_dot2 against ones).
+  auto accumulate = [&](int b, const f32x16 (&pt)[2], bool rescale, float corr) __attribute__((always_inline)) {
     if (rescale) {
 #pragma unroll
       for (int c = 0; c < DTILES; ++c)
@@ -517,6 +536,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int key_hi = DMA ? opaque(v_key_hi) : 0;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
+      u32x4 pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pb[e] = Ops::pack2(pt[ks / 2][(ks % 2) * 8 + 2 * e], pt[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
 #pragma unroll
       for (int c = 0; c < DTILES; ++c) {
         const char* rows = reinterpret_cast<const char*>(v_lds + ks * 16 * VROW);
@@ -527,8 +549,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         const u32x2 lo = lds_read_tr(vlo);
         const u32x2 hi = lds_read_tr(vhi);
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
-        acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb[ks]), acc_o[c]);
+        acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
       }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lsum = Ops::sum2(pb[e], lsum);
     }
   };
   const int niter = (ntiles + 1) / 2;  // tiles per key group (the last of group 1 may not exist)
@@ -576,7 +600,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     int32_t next_k = page_slot(tile_page(kg + 6));     // K of tile j + 6
     if (kg == 1) phase_barrier();
     f32x16 sacc[2];
-    u32x4 pb[4];
     bool rescale = false;
     float corr = 1.f;
     for (int t = 0; t <= niter; ++t) {
@@ -586,7 +609,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       __builtin_amdgcn_s_setprio(1);
       // One site each for P V and S: accumulators updated on two paths
       // would be given two register sets.
-      if (t >= 1 && active(j - 2)) accumulate(1 - P, pb, rescale, corr);
+      if (t >= 1 && active(j - 2)) accumulate(1 - P, sacc, rescale, corr);
       __builtin_amdgcn_sched_barrier(0);
       if (t < niter && active(j)) scores(P, sacc);
       __builtin_amdgcn_s_setprio(0);
@@ -603,7 +626,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         __builtin_amdgcn_sched_barrier(0);
       };
       if (active(j)) {
-        rescale = softmax(j * kBN, sacc, pb, corr, stage);
+        rescale = softmax(j * kBN, sacc, corr, stage);
       } else {
 #pragma unroll
         for (int n = 0; n < 8; ++n) stage(n);
@@ -641,11 +664,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       const int j = 2 * it + kg;
       if (active(j)) {
         f32x16 sacc[2];
-        u32x4 pb[4];
         float corr = 1.f;
         scores(it & 1, sacc);
-        const bool rescale = softmax(j * kBN, sacc, pb, corr, [](int) {});
-        accumulate(it & 1, pb, rescale, corr);
+        const bool rescale = softmax(j * kBN, sacc, corr, [](int) {});
+        accumulate(it & 1, sacc, rescale, corr);
       }
       if (j + 2 < ntiles) store_tile((it + 1) & 1);
       __syncthreads();
