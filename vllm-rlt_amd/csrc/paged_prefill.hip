@@ -28,6 +28,7 @@
 // backends use for prefill.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "common.hpp"
 #include "mfma.hpp"
@@ -229,7 +230,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();
     s_scan[tid] = tid < ns ? s_qt[s_order[tid]] : 0;
     __syncthreads();
-    for (int off = 1; off < kRankSeqs; off <<= 1) {  // inclusive scan
+    for (int off = 1; off < ns; off <<= 1) {  // inclusive scan of the ns ranked entries
       const int v = tid >= off ? s_scan[tid - off] : 0;
       __syncthreads();
       s_scan[tid] += v;
@@ -416,64 +417,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
   float m = -INFINITY;
   // This lane's share of its query's row sum: the keys it holds, summed from
-  // the rounded P that also weights V (v_dot2 against ones, in the softmax
-  // phase; the lane 32 away holds the other keys).
+  // the rounded P that also weights V (v_dot2 against ones, next to the P V
+  // MFMAs; the lane 32 away holds the other keys).
   float lsum = 0.f;
 
   // Whether the wave computes tile j: it exists and holds a key visible to
   // one of the wave's queries.  Once false it stays false for later tiles.
   auto active = [&](int j) { return j < ntiles && wave_live && j * kBN <= wave_last_key; };
-  // S^T = K Q^T for the tile's two 32-key halves, as two interleaved MFMA
-  // chains (each MFMA has the other chain's MFMA to wait out its K read).
+  // Register-staged path (padded rows): S^T = K Q^T for the tile's two 32-key
+  // halves, as two interleaved MFMA chains.
   auto scores = [&](int b, f32x16 (&sacc)[2]) __attribute__((always_inline)) {
     const uint16_t* k_lds = group_lds + b * (KT + VT);
-    const int key = DMA ? opaque(k_key) : 0;
     f32x16 c[2] = {{}, {}};
-    if constexpr (DMA) {
-      // The K reads run kAhead k-steps ahead of their MFMAs, pinned in that
-      // order: an LDS read takes longer than the two MFMAs of one k-step, so
-      // reads issued one step ahead leave every step waiting for its operand.
-      constexpr int kAhead = 3;
-      auto rd = [&](int ks, int hh) __attribute__((always_inline)) {
-        const char* row = reinterpret_cast<const char*>(k_lds + hh * 32 * KROW);
-        return *reinterpret_cast<const u32x4*>(row + (((ks << 5) ^ key) + k_base));
-      };
-      u32x4 kq[kAhead + 1][2];
 #pragma unroll
-      for (int ks = 0; ks < kAhead; ++ks)
+    for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) kq[ks][hh] = rd(ks, hh);
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        if (ks + kAhead < KSTEPS)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) kq[(ks + kAhead) % (kAhead + 1)][hh] = rd(ks + kAhead, hh);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-          c[hh] = Ops::mma(as_v8<V8>(kq[ks % (kAhead + 1)][hh]), as_v8<V8>(qb[ks]), c[hh]);
-        __builtin_amdgcn_sched_barrier(0);
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
+        c[hh] = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c[hh]);
       }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const u32x4 kv = *reinterpret_cast<const u32x4*>(&k_lds[(hh * 32 + col) * KROW + ks * 16 + half * 8]);
-          c[hh] = Ops::mma(as_v8<V8>(kv), as_v8<V8>(qb[ks]), c[hh]);
-        }
-    }
     sacc[0] = c[0];
     sacc[1] = c[1];
   };
   // Online softmax of tile key0: mask (diagonal tiles and the chunk's last
-  // rows only), tile maximum, exponentials.  Leaves P^T in fp32 in sacc;
-  // accumulate() rounds it to T one 16-key k-step at a time, next to that
-  // step's MFMAs, where the VALU work hides under them instead of lengthening
-  // this phase.  Element r of half hh holds key
+  // rows only), tile maximum, exponentials.  Leaves P^T in fp32 in sacc; the
+  // P V step rounds it to T one 16-key k-step at a time, next to that step's
+  // MFMAs, where the VALU work hides under them instead of lengthening this
+  // phase.  Element r of half hh holds key
   // key0 + 32hh + 8(r/4) + 4half + r%4.  When the running maximum moves it
   // returns true with the accumulators' factor in corr, which the row sum takes
-  // here and acc_o in accumulate().  hook(0) .. hook(7) run
+  // here and acc_o in the P V step.  hook(0) .. hook(7) run
   // at fixed points along the way (the staging loads of the direct-to-LDS
   // path, spread out so that they never queue up behind one another).
   auto softmax = [&](int key0, f32x16 (&sacc)[2], float& corr, auto&& hook)
@@ -521,9 +494,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
     return rescale;
   };
-  // O^T = O^T * corr (when softmax() moved the maximum) + V^T P^T over the
-  // tile's four 16-key k-steps.  Each step packs its P^T operand to T and
-  // adds exactly those rounded values to the row sum (v_dot2 against ones).
+  // Register-staged path: O^T = O^T * corr (when softmax() moved the maximum)
+  // + V^T P^T over the tile's four 16-key k-steps.  Each step packs its P^T
+  // operand to T and adds exactly those rounded values to the row sum (v_dot2
+  // against ones).
   auto accumulate = [&](int b, const f32x16 (&pt)[2], bool rescale, float corr) __attribute__((always_inline)) {
     if (rescale) {
 #pragma unroll
@@ -532,8 +506,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
     }
     const uint16_t* v_lds = group_lds + b * (KT + VT) + KT;
-    const int key = DMA ? opaque(v_key) : 0;
-    const int key_hi = DMA ? opaque(v_key_hi) : 0;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       u32x4 pb;
@@ -541,13 +513,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int e = 0; e < 4; ++e) pb[e] = Ops::pack2(pt[ks / 2][(ks % 2) * 8 + 2 * e], pt[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
 #pragma unroll
       for (int c = 0; c < DTILES; ++c) {
-        const char* rows = reinterpret_cast<const char*>(v_lds + ks * 16 * VROW);
-        const uint16_t* vlo = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key) + v_base_lo))
-                                  : &v_lds[tr_off + ks * 16 * VROW + c * 32];
-        const uint16_t* vhi = DMA ? reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ key_hi) + v_base_hi))
-                                  : vlo + 8 * VROW;
+        const uint16_t* vlo = &v_lds[tr_off + ks * 16 * VROW + c * 32];
         const u32x2 lo = lds_read_tr(vlo);
-        const u32x2 hi = lds_read_tr(vhi);
+        const u32x2 hi = lds_read_tr(vlo + 8 * VROW);
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
         acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb), acc_o[c]);
       }
@@ -555,11 +523,90 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int e = 0; e < 4; ++e) lsum = Ops::sum2(pb[e], lsum);
     }
   };
+  // Direct-to-LDS path: one MFMA phase as a single stream in issue order --
+  // the P V MFMAs of tile j - 2 (k = 0..15: k-step k / 4, output tile k % 4),
+  // then the S MFMAs of tile j (k = 16..31: k-step (k - 16) / 2, key half
+  // k % 2).  Each MFMA's A operand (two transposing V reads, or one K read) is
+  // read kStreamAhead MFMAs before it, and every read, pack and MFMA is pinned
+  // in that order: left to itself the scheduler groups the reads of several
+  // k-steps, and each MFMA's wait then covers reads it does not use.  P^T of
+  // k-step ks is rounded to T one k-step early and added to the row sum
+  // (v_dot2 against ones) after that step's MFMAs.
+  constexpr int kStreamAhead = 3;
+  auto mfma_phase = [&](auto pv_tag, auto s_tag, int b_pv, int b_s, f32x16 (&sacc)[2], bool rescale, float corr)
+                        __attribute__((always_inline)) {
+    constexpr bool PV = decltype(pv_tag)::value, S = decltype(s_tag)::value;
+    constexpr int K0 = PV ? 0 : 16, K1 = S ? 32 : 16, R = kStreamAhead + 1;
+    if (PV && rescale) {
+#pragma unroll
+      for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[c][r] *= corr;
+    }
+    const char* v_rows = reinterpret_cast<const char*>(group_lds + b_pv * (KT + VT) + KT);
+    const char* k_rows = reinterpret_cast<const char*>(group_lds + b_s * (KT + VT));
+    const int vk = opaque(v_key), vk_hi = opaque(v_key_hi), kk = opaque(k_key);
+    auto read = [&](int k) __attribute__((always_inline)) {
+      if (k < 16) {
+        const int ks = k >> 2, c = k & 3;
+        const char* rows = v_rows + ks * 16 * VROW * 2;
+        const u32x2 lo = lds_read_tr(reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ vk) + v_base_lo)));
+        const u32x2 hi = lds_read_tr(reinterpret_cast<const uint16_t*>(rows + (((c << 6) ^ vk_hi) + v_base_hi)));
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+      const int ks = (k - 16) >> 1, hh = k & 1;
+      return *reinterpret_cast<const u32x4*>(k_rows + hh * 32 * KROW * 2 + (((ks << 5) ^ kk) + k_base));
+    };
+    auto pack = [&](int ks) __attribute__((always_inline)) {
+      u32x4 pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pb[e] = Ops::pack2(sacc[ks / 2][(ks % 2) * 8 + 2 * e], sacc[ks / 2][(ks % 2) * 8 + 2 * e + 1]);
+      return pb;
+    };
+    u32x4 ring[R];
+    u32x4 pb[4];
+    f32x16 c[2] = {{}, {}};
+#pragma unroll
+    for (int k = K0; k < K0 + kStreamAhead; ++k) {
+      ring[k % R] = read(k);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (PV) pb[0] = pack(0);
+#pragma unroll
+    for (int k = K0; k < K1; ++k) {
+      if (k + kStreamAhead < K1) ring[(k + kStreamAhead) % R] = read(k + kStreamAhead);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k < 16) {
+        acc_o[k & 3] = Ops::mma(as_v8<V8>(ring[k % R]), as_v8<V8>(pb[k >> 2]), acc_o[k & 3]);
+        if ((k & 3) == 1 && k < 12) pb[(k >> 2) + 1] = pack((k >> 2) + 1);
+        if ((k & 3) == 3) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) lsum = Ops::sum2(pb[k >> 2][e], lsum);
+        }
+      } else {
+        const int ks = (k - 16) >> 1, hh = k & 1;
+        c[hh] = Ops::mma(as_v8<V8>(ring[k % R]), as_v8<V8>(qb[ks]), c[hh]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (S) {
+      sacc[0] = c[0];
+      sacc[1] = c[1];
+    }
+  };
   const int niter = (ntiles + 1) / 2;  // tiles per key group (the last of group 1 may not exist)
 
   if constexpr (DMA) {
     const int fill = min(4 * ntiles, kTablePages);
     for (int i = tid; i < fill; i += 512) page_ids[i] = trow[min(i, last_page)];
+    {
+      // The V tile of buffer 1, which the first MFMA phase reads (times P = 0)
+      // before any tile is staged there: zero, so no stale NaN reaches acc_o.
+      u32x4* vz = reinterpret_cast<u32x4*>(group_lds + (KT + VT) + KT);
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      for (int i = tid & 255; i < VT / 8; i += 256) vz[i] = zero;
+    }
     __syncthreads();
     // Ping-pong.  Iteration t of key group g handles tile j = 2t + g in two
     // phases: an MFMA phase (P V of tile j - 2, then S of tile j) and a
@@ -599,7 +646,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     uint32_t id_k = page_id(tile_page(kg + 4));        // K of tile j + 4
     int32_t next_k = page_slot(tile_page(kg + 6));     // K of tile j + 6
     if (kg == 1) phase_barrier();
-    f32x16 sacc[2];
+    f32x16 sacc[2] = {{}, {}};  // P of tile j - 2: none before the first phase
     bool rescale = false;
     float corr = 1.f;
     for (int t = 0; t <= niter; ++t) {
@@ -607,11 +654,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       const int P = t & 1;
       load_barrier();
       __builtin_amdgcn_s_setprio(1);
-      // One site each for P V and S: accumulators updated on two paths
-      // would be given two register sets.
-      if (t >= 1 && active(j - 2)) accumulate(1 - P, sacc, rescale, corr);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t < niter && active(j)) scores(P, sacc);
+      // One site for the whole phase (accumulators updated on two paths would
+      // be given two register sets).  At t = 0 the P V half multiplies a
+      // zeroed V buffer by P = 0; past the wave's last tile, and at t = niter,
+      // the S half's scores are never used.
+      if (t == 0 ? active(j) : active(j - 2))
+        mfma_phase(std::true_type{}, std::true_type{}, 1 - P, P, sacc, rescale, corr);
       __builtin_amdgcn_s_setprio(0);
       if (t == niter) break;
       phase_barrier();
