@@ -250,6 +250,27 @@ def prefill_case(dtype, seed=712):
     return q, key_pool, value_pool, tables, lengths, cu, row_tables, row_lengths
 
 
+@pytest.mark.parametrize("num_seqs", [137, 512, 513])
+def test_mfma_prefill_many_sequences(num_seqs):
+    # The ranked work list sorts and scans the sequences in the workgroup (up to
+    # 512 of them: 137 and 512 are ranked, 513 falls back to the direct list),
+    # with short chunks over short prefixes so that most query tiles are alone.
+    from vllm_rlt_amd import ops
+
+    g = torch.Generator().manual_seed(7000 + num_seqs)
+    prefixes = [int(x) for x in torch.randint(0, 80, (num_seqs,), generator=g)]
+    chunks = [int(x) for x in torch.randint(1, 5, (num_seqs,), generator=g)]
+    q, kp, vp, tables, lens, cu, row_tables, row_lengths = ragged_prefill_case(
+        torch.bfloat16, 8, 8, 128, prefixes, chunks, num_seqs
+    )
+    print(f"[prefill many] num_seqs={num_seqs} rows={sum(chunks)}", flush=True)
+    out = ops.paged_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), cu.cuda(), max(chunks))
+    torch.cuda.synchronize()
+    expect = paged_attention_cpu(q, kp, vp, row_tables, row_lengths)
+    atol, rtol = TOL[torch.bfloat16]
+    torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_packed_prefill_matches_per_token_oracle(dtype):
     from vllm_rlt_amd.paged_attention import HipPagedAttention
