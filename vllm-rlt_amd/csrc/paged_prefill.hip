@@ -3,13 +3,15 @@
 // Sequence s owns query rows [cu[s], cu[s+1]); its keys end at its last query
 // position, so chunk query i sees keys [0, len_k[s] - n_q + i].
 //
-// MFMA path (bf16 / fp16, head_dim 64 or 128, page 16).  A workgroup owns 128
-// query rows of one (sequence, query head); each of its 4 waves owns 32.  Key
-// tiles of 64 tokens (4 pages) are staged in LDS -- K and V row-major, rows
-// padded against bank conflicts -- with the next tile's global loads in
-// registers while the current tile computes.  Per tile a wave forms
-// S^T = K Q^T with v_mfma_f32_32x32x16 (A = K rows from LDS, B = its 32 q rows
-// from registers), so every lane holds 16 keys of one query: the online
+// MFMA path (bf16 / fp16, head_dim 64 or 128, page 16).  A workgroup of 8
+// waves owns 128 query rows of one (sequence, query head): two key groups of 4
+// waves take the even and the odd 64-token key tiles (4 pages each), each wave
+// 32 rows, and merge at the end.  Tiles are staged in LDS: for head_dim 128
+// straight from global memory (swizzled rows, see below) with the two groups
+// in ping-pong -- one group's MFMA phase beside the other's softmax phase on
+// every SIMD -- otherwise through registers into padded rows.  Per tile a wave
+// forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = K rows from LDS, B = its 32
+// q rows from registers), so every lane holds 16 keys of one query: the online
 // softmax needs one exchange with the lane 32 away.  The exponentiated scores,
 // rounded to the storage type, are already the B operand of O^T += V^T P^T:
 // within each 16-key k-step lane half h element e holds key
