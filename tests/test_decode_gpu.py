@@ -250,6 +250,41 @@ def prefill_case(dtype, seed=712):
     return q, key_pool, value_pool, tables, lengths, cu, row_tables, row_lengths
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mfma_prefill_empty_and_single_token_sequences(dtype):
+    # Sequences with no new token (equal cu_seqlens entries) between others,
+    # a one-token chunk over an empty prefix (one key) and one over a long
+    # prefix: the empty sequences own no rows, and every row of the others
+    # matches the per-token oracle.
+    from vllm_rlt_amd import ops
+
+    prefixes, chunks = [40, 0, 700, 0, 1500, 33], [0, 1, 0, 130, 1, 0]
+    lens = [p + c for p, c in zip(prefixes, chunks)]
+    live = [i for i, c in enumerate(chunks) if c > 0]
+    q, kp, vp, tables, _, cu, row_tables, row_lengths = ragged_prefill_case(
+        dtype, 16, 16, 128, [prefixes[i] for i in live], [chunks[i] for i in live], 11
+    )
+    # Re-pack with the empty sequences in place: their tables point at valid pages, their q rows are none.
+    full_tables = torch.full((len(chunks), tables.shape[1]), -1, dtype=torch.int32)
+    for k, i in enumerate(live):
+        full_tables[i] = tables[k]
+    for i, c in enumerate(chunks):
+        if c == 0:
+            pages = -(-lens[i] // 16)
+            full_tables[i, :pages] = tables[0, 0]
+    full_cu = torch.tensor([0] + torch.tensor(chunks).cumsum(0).tolist(), dtype=torch.int32)
+    print(f"[prefill empty] chunks={chunks} prefixes={prefixes} {dtype}", flush=True)
+    out = torch.full_like(q, 7.0).cuda()
+    ops.paged_prefill(
+        q.cuda(), kp.cuda(), vp.cuda(), full_tables.cuda(), torch.tensor(lens, dtype=torch.int32).cuda(),
+        full_cu.cuda(), max(chunks), out=out,
+    )
+    torch.cuda.synchronize()
+    expect = paged_attention_cpu(q, kp, vp, row_tables, row_lengths)
+    atol, rtol = TOL[dtype]
+    torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
+
+
 @pytest.mark.parametrize("num_seqs", [137, 512, 513])
 def test_mfma_prefill_many_sequences(num_seqs):
     # The ranked work list sorts and scans the sequences in the workgroup (up to
