@@ -17,7 +17,16 @@ Three fixtures pin what the reference's own tests leave open:
       reference's rotary embedding (OuroRotaryEmbedding, vllm_rlt/models/
       ouro.py:39-70) and of the q/k rotation q * cos + _rotate_half(q) * sin
       (ouro.py:73-75, 108-109) in bf16 / fp16 / fp32.
+  pd_segments.json -- the exact, ordered output lists of the reference's
+      kv_segments and partition_segments (vllm_rlt/pd/transport.py:18-68) for
+      several pool geometries, multi-depth tables and token ranges (whole
+      pages, partial first/last pages, single tokens), and its error messages
+      for invalid ranges.
 The fixture files hold data only (inputs and outputs).
+
+Fixture names given after the reference path select which files are
+rewritten (default: all), so one fixture can be added without touching the
+bytes of the others.
 
 The reference tree is read-only: bytecode writing is switched off before the
 reference is put on sys.path, so importing it leaves no __pycache__ there.
@@ -195,15 +204,103 @@ def rotary_cases():
     return arrays
 
 
+# Segment cases: pool geometry, tables (one per storage depth), [start, end)
+# ranges, and (byte_limit, descriptor_limit) pairs for partition_segments.
+SEGMENT_GEOMETRIES = [
+    # block_size, num_layers, token_bytes, num_blocks, key_ptr, value_ptr, tables
+    (4, 3, 64, 24, 0, 10**9, [[5, 2, 9], [11, 0, 7], [3, 4, 8]]),
+    (16, 24, 4096, 4096, 1 << 40, (1 << 40) + (1 << 36), [[4095, 17, 1024, 3], [8, 9, 10, 11]]),
+    (1, 2, 32, 6, 4096, 8192, [[5, 0, 3, 1]]),
+    (8, 1, 16, 10, 0, 1 << 20, [[9, 1], [2, 3], [4, 5], [6, 7]]),
+]
+SEGMENT_RANGES = {
+    4: [(2, 9), (0, 8), (4, 5), (0, 1), (3, 12), (0, 12), (11, 12), (1, 3)],
+    16: [(0, 64), (5, 6), (15, 17), (16, 48), (3, 61), (0, 1), (63, 64)],
+    1: [(0, 4), (2, 3), (1, 4)],
+    8: [(0, 16), (7, 9), (8, 16), (1, 15)],
+}
+PARTITION_LIMITS = [(333, 3), (1 << 30, 1), (64, 1000), (4096 * 16 + 5, 4), (7, 2), (1 << 20, 7)]
+MAX_PIECES = 400  # limits that would cut a case into more pieces are skipped
+
+
+def segment_cases():
+    from vllm_rlt.pd.transport import kv_segments, partition_segments
+
+    cases = []
+    for page, layers, token, blocks, key_ptr, value_ptr, tables in SEGMENT_GEOMETRIES:
+        info = dict(
+            block_size=page,
+            num_layers=layers,
+            token_bytes=token,
+            layer_bytes=page * token,
+            block_bytes=layers * page * token,
+            num_blocks=blocks,
+            key_ptr=key_ptr,
+            value_ptr=value_ptr,
+            device=0,
+        )
+        for start, end in SEGMENT_RANGES[page]:
+            segments = [list(s) for s in kv_segments(info, tables, start, end)]
+            partitions = []
+            total = sum(n for _, n, _ in segments)
+            for byte_limit, descriptor_limit in PARTITION_LIMITS:
+                if total // byte_limit + len(segments) > MAX_PIECES:
+                    continue
+                # The reference test pairs a list with itself; shift the target so the
+                # pairing of source and target pieces is visible in the fixture.
+                target = [(a + 12345, n, 1) for a, n, _ in segments]
+                parts = partition_segments([tuple(s) for s in segments], target, byte_limit, descriptor_limit)
+                partitions.append(
+                    {
+                        "byte_limit": byte_limit,
+                        "descriptor_limit": descriptor_limit,
+                        "parts": [[[list(x) for x in src], [list(x) for x in dst], n] for src, dst, n in parts],
+                    }
+                )
+            cases.append(
+                {"info": info, "tables": tables, "start": start, "end": end, "segments": segments, "partitions": partitions}
+            )
+    errors = []
+    page, layers, token, blocks, key_ptr, value_ptr, tables = SEGMENT_GEOMETRIES[0]
+    info = dict(cases[0]["info"])
+    for name, use_info, use_tables, start, end in [
+        ("empty", info, tables, 5, 5),
+        ("negative", info, tables, -1, 3),
+        ("past_allocation", info, tables, 0, 13),
+        ("block_outside_pool", dict(info, num_blocks=9), tables, 0, 12),
+        ("second_table_short", info, [tables[0] + [1], [2]], 0, 13),
+    ]:
+        try:
+            list(kv_segments(use_info, use_tables, start, end))
+            message = None
+        except ValueError as e:
+            message = str(e)
+        errors.append({"case": name, "info": use_info, "tables": use_tables, "start": start, "end": end, "error": message})
+    try:
+        list(partition_segments([(0, 8, 0), (64, 8, 0)], [(0, 8, 0)], 100, 4))
+        mismatch = None
+    except ValueError as e:
+        mismatch = str(e)
+    return {"cases": cases, "errors": errors, "partition_mismatch_error": mismatch}
+
+
+FIXTURES = {
+    "allocator_trace.json": lambda path: path.write_text(json.dumps(allocator_trace(), indent=1)),
+    "paged_attention_cpu.npz": lambda path: np.savez_compressed(path, **attention_cases()),
+    "rotary_cpu.npz": lambda path: np.savez_compressed(path, **rotary_cases()),
+    "pd_segments.json": lambda path: path.write_text(json.dumps(segment_cases())),
+}
+
+
 def main():
     reference = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    names = sys.argv[2:] or list(FIXTURES)
     sys.dont_write_bytecode = True  # never write .pyc files into the reference tree
     sys.path.insert(0, reference)
     torch.set_num_threads(1)
-    (OUT / "allocator_trace.json").write_text(json.dumps(allocator_trace(), indent=1))
-    np.savez_compressed(OUT / "paged_attention_cpu.npz", **attention_cases())
-    np.savez_compressed(OUT / "rotary_cpu.npz", **rotary_cases())
-    print("wrote", OUT / "allocator_trace.json", OUT / "paged_attention_cpu.npz", OUT / "rotary_cpu.npz")
+    for name in names:
+        FIXTURES[name](OUT / name)
+        print("wrote", OUT / name)
 
 
 if __name__ == "__main__":

@@ -1,12 +1,19 @@
 """Segment format of page transfers (CPU): kv_segments and partition_segments.
 
-The byte ranges are pinned the way the reference's own test pins them
-(tests/test_pd.py:47-82): the union of the segments must be exactly the bytes
-of tokens [start, end) at every layer, depth and K/V plane, computed by brute
-force from the closed-form address (block, layer, token); partitions must
+The exact, ordered output of both functions is pinned by
+tests/golden/pd_segments.json, recorded from the reference's own
+kv_segments / partition_segments (vllm_rlt/pd/transport.py:18-68): the order
+is part of the format, since a peer pairs its segments with ours one by one.
+Beyond that, the byte ranges are pinned the way the reference's own test pins
+them (tests/test_pd.py:47-82): the union of the segments must be exactly the
+bytes of tokens [start, end) at every layer, depth and K/V plane, computed by
+brute force from the closed-form address (block, layer, token); partitions must
 conserve bytes and respect both limits.  Known page ids come from the host
 page book, which reproduces the reference's allocator page for page.
 """
+
+import json
+from pathlib import Path
 
 import pytest
 
@@ -100,3 +107,55 @@ def test_invalid_ranges_and_mismatched_geometry_raise():
     segs = list(kv_segments(info, tables, 0, 6))
     with pytest.raises(ValueError, match="incompatible"):
         list(partition_segments(segs, segs[:-1], 1000, 10))
+
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "pd_segments.json").read_text())
+
+
+@pytest.mark.parametrize("case", range(len(GOLDEN["cases"])))
+def test_segment_lists_equal_the_reference_recording(case):
+    c = GOLDEN["cases"][case]
+    segments = kv_segments(c["info"], c["tables"], c["start"], c["end"])
+    assert [list(s) for s in segments] == c["segments"]
+    # Union of the recorded segments is exactly the brute-force byte set, so the
+    # fixture itself agrees with the closed-form address map.
+    if sum(n for _, n, _ in segments) <= 1 << 16:
+        covered = set()
+        for address, size, _ in segments:
+            covered.update(range(address, address + size))
+        assert covered == brute_force(c["info"], c["tables"], c["start"], c["end"])
+    assert c["partitions"], "every case carries at least one partition recording"
+    for p in c["partitions"]:
+        target = [(a + 12345, n, 1) for a, n, _ in segments]
+        parts = partition_segments(segments, target, p["byte_limit"], p["descriptor_limit"])
+        got = [[[list(x) for x in src], [list(x) for x in dst], n] for src, dst, n in parts]
+        assert got == p["parts"]
+
+
+@pytest.mark.parametrize("entry", GOLDEN["errors"], ids=lambda e: e["case"])
+def test_segment_errors_match_the_reference(entry):
+    if entry["error"] is None:
+        kv_segments(entry["info"], entry["tables"], entry["start"], entry["end"])
+    else:
+        with pytest.raises(ValueError) as err:
+            kv_segments(entry["info"], entry["tables"], entry["start"], entry["end"])
+        assert str(err.value) == entry["error"]
+
+
+def test_partition_mismatch_message_matches_the_reference():
+    with pytest.raises(ValueError) as err:
+        partition_segments([(0, 8, 0), (64, 8, 0)], [(0, 8, 0)], 100, 4)
+    assert str(err.value) == GOLDEN["partition_mismatch_error"]
+
+
+def test_planted_order_mistakes_fail_the_golden():
+    """Orders a plausible rewrite could produce (V before K, layers outermost,
+    tables innermost) cover the same bytes but fail the recorded list."""
+    c = next(c for c in GOLDEN["cases"] if len(c["tables"]) > 1 and c["start"] % c["info"]["block_size"])
+    segs = [tuple(s) for s in c["segments"]]
+    info = c["info"]
+    v_first = sorted(segs, key=lambda s: (s[0] < info["value_ptr"], s[0]))
+    by_address = sorted(segs)
+    for wrong in (v_first, by_address, segs[::-1]):
+        assert sorted(wrong) == sorted(segs)
+        assert [list(s) for s in wrong] != c["segments"]

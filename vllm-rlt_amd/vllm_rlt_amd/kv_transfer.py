@@ -1,6 +1,7 @@
 """Page export / import: preemption snapshots and the prefill-to-decode segment format.
 
-The byte-range format is the reference's (vllm_rlt/pd/transport.py:18-68): a
+The byte-range format is the reference's (vllm_rlt/pd/transport.py:18-68),
+because a decode-side peer pairs its segments with ours one by one: a
 request's valid token range [start, end) becomes one segment per whole page
 (all layers, one contiguous block) and one per layer for a partially valid
 page, for K and V and every storage depth; partition_segments bounds each
@@ -19,7 +20,6 @@ and rlt_kv_import_pages restores them.
 from __future__ import annotations
 
 from copy import deepcopy
-from itertools import zip_longest
 
 import torch
 
@@ -49,57 +49,92 @@ def transfer_info(cache, hidden: torch.Tensor | None = None) -> dict:
     return info
 
 
-def kv_segments(info: dict, tables, start: int, end: int):
-    """(address, bytes, device) ranges holding tokens [start, end) of every table (depth).
+def _page_pieces(info: dict, lo: int, hi: int) -> list[tuple[int, int]]:
+    """(offset inside one page's block, bytes) pieces that hold tokens [lo, hi) of the page.
 
-    A fully valid page is one segment (all layers); a partial page is one
-    segment per layer covering only its valid tokens, so unused tail bytes are
-    never sent (vllm_rlt/pd/transport.py:18-46).
+    All tokens valid: the whole block (every layer) is one piece.  Otherwise
+    each layer's slice of the page holds the tokens at the same place, so the
+    page contributes one piece per layer, in layer order.
+    """
+    if hi - lo == info["block_size"]:
+        return [(0, info["block_bytes"])]
+    first, size = lo * info["token_bytes"], (hi - lo) * info["token_bytes"]
+    stride = info["layer_bytes"]
+    return [(first + layer * stride, size) for layer in range(info["num_layers"])]
+
+
+def kv_segments(info: dict, tables, start: int, end: int) -> list[tuple[int, int, int]]:
+    """(address, bytes, device) ranges that hold tokens [start, end) of every table.
+
+    The order is part of the format, since a peer pairs its own segments with
+    these one by one (vllm_rlt/pd/transport.py:18-46, paired at
+    vllm_rlt/pd/worker.py:214-229): tables (storage depths) in order; within a
+    table, pages in logical order; within a page, the key pool's pieces, then
+    the value pool's.  A page whose tokens are all in the range is a single
+    segment of its whole block; a partially covered page gives one segment per
+    layer, so bytes of tokens outside the range are never sent.  Every table
+    is checked before any segment is returned, with the reference's messages.
     """
     page = info["block_size"]
     if not 0 <= start < end:
         raise ValueError("invalid KV range")
+    first_page, last_page = start // page, (end - 1) // page
+    # The valid token window of each touched page, relative to that page.
+    windows = [
+        (logical, max(start, logical * page) - logical * page, min(end, (logical + 1) * page) - logical * page)
+        for logical in range(first_page, last_page + 1)
+    ]
+    pieces = [_page_pieces(info, lo, hi) for _, lo, hi in windows]
+    bases = (info["key_ptr"], info["value_ptr"])
+    device, block_bytes, num_blocks = info["device"], info["block_bytes"], info["num_blocks"]
+    out = []
     for table in tables:
-        if end > len(table) * page:
+        if len(table) * page < end:
             raise ValueError("KV range exceeds allocation")
-        for logical in range(start // page, (end - 1) // page + 1):
-            block = table[logical]
-            if not 0 <= block < info["num_blocks"]:
-                raise ValueError("physical block outside registered pool")
-            lo = max(start - logical * page, 0)
-            hi = min(end - logical * page, page)
-            for base in (info["key_ptr"], info["value_ptr"]):
-                address = base + block * info["block_bytes"]
-                if lo == 0 and hi == page:
-                    yield (address, info["block_bytes"], info["device"])
-                else:
-                    for layer in range(info["num_layers"]):
-                        yield (
-                            address + layer * info["layer_bytes"] + lo * info["token_bytes"],
-                            (hi - lo) * info["token_bytes"],
-                            info["device"],
-                        )
+        blocks = [table[logical] for logical, _, _ in windows]
+        if any(not 0 <= b < num_blocks for b in blocks):
+            raise ValueError("physical block outside registered pool")
+        for block, page_pieces in zip(blocks, pieces):
+            out.extend(
+                (base + block * block_bytes + offset, size, device)
+                for base in bases
+                for offset, size in page_pieces
+            )
+    return out
 
 
 def partition_segments(source, target, byte_limit: int, descriptor_limit: int):
-    """Pair source and target segments into transfers of at most byte_limit bytes and
-    descriptor_limit descriptors, splitting segments where needed (vllm_rlt/pd/transport.py:49-68)."""
-    local, remote, size = [], [], 0
-    for src, dst in zip_longest(source, target):
-        if src is None or dst is None or src[1] != dst[1]:
-            raise ValueError("incompatible source/target KV geometry")
+    """Cut paired source/target segments into transfers (vllm_rlt/pd/transport.py:49-68).
+
+    Returns a list of (source pieces, target pieces, bytes).  The pairs are
+    laid end to end as one byte stream and cut greedily: a transfer closes as
+    soon as it holds byte_limit bytes or descriptor_limit pieces, and a
+    segment that straddles a cut continues, at the same offset on both sides,
+    in the next transfer.  Zero-byte segments produce no piece.  Each pair must
+    have equal sizes ("incompatible source/target KV geometry" otherwise,
+    checked for every pair before anything is returned).
+    """
+    source, target = list(source), list(target)
+    if len(source) != len(target) or any(s[1] != t[1] for s, t in zip(source, target)):
+        raise ValueError("incompatible source/target KV geometry")
+    if byte_limit <= 0 or descriptor_limit <= 0:
+        raise ValueError("transfer limits must be positive")
+    transfers = []
+    pending_src, pending_dst, room = [], [], byte_limit
+    for (s_addr, size, s_dev), (t_addr, _, t_dev) in zip(source, target):
         offset = 0
-        while offset < src[1]:
-            amount = min(src[1] - offset, byte_limit - size)
-            local.append((src[0] + offset, amount, src[2]))
-            remote.append((dst[0] + offset, amount, dst[2]))
-            size += amount
-            offset += amount
-            if size == byte_limit or len(local) == descriptor_limit:
-                yield local, remote, size
-                local, remote, size = [], [], 0
-    if local:
-        yield local, remote, size
+        while offset < size:
+            take = min(size - offset, room)
+            pending_src.append((s_addr + offset, take, s_dev))
+            pending_dst.append((t_addr + offset, take, t_dev))
+            offset += take
+            room -= take
+            if room == 0 or len(pending_src) == descriptor_limit:
+                transfers.append((pending_src, pending_dst, byte_limit - room))
+                pending_src, pending_dst, room = [], [], byte_limit
+    if pending_src:
+        transfers.append((pending_src, pending_dst, byte_limit - room))
+    return transfers
 
 
 def _inside(address: int, size: int, regions) -> bool:
