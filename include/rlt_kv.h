@@ -268,6 +268,12 @@ int rlt_paged_decode_no_alloc(const void* q, const int64_t* q_strides, const voi
                               int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                               int64_t num_blocks, float scale, int dtype, void* stream);
 
+/* Device bytes the library holds on every device it runs on, whether or not
+ * rlt_paged_decode_no_alloc is called: the static scratch array above (64 MiB),
+ * part of the code object loaded on the device.  No counterpart in the
+ * reference; memory planners subtract it from the KV budget. */
+int64_t rlt_static_device_bytes(void);
+
 /* Rows per launch of rlt_paged_decode_no_alloc for this head geometry (0 when
  * even one row exceeds the static scratch or the heads are invalid). */
 int64_t rlt_paged_decode_no_alloc_rows_per_launch(int64_t num_q_heads, int64_t num_kv_heads,

@@ -113,6 +113,22 @@ def test_no_alloc_decode_rejects_rows_larger_than_the_scratch():
     lib = _native.load()
     # 64 query heads x head_dim 4096: one row needs just over 64 MiB of partials.
     assert lib.rlt_paged_decode_no_alloc_rows_per_launch(64, 64, 4096) == 0
-    s = _native.int64_array([1, 1, 1, 1])
-    rc = lib.rlt_paged_decode_no_alloc(1, s, 1, 1, s, 1, 1, 1, 1, 1, s, 1, 64, 64, 4096, 16, 1, 1.0, 2, None)
+    # Real device buffers of the declared shapes (one row of one token over one
+    # page), so that even a launch past a broken size check reads and writes
+    # valid memory and the assert, not the device, reports the regression.
+    hq, d, page = 64, 4096, 16
+    q = torch.zeros(1, hq, d, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros_like(q)
+    kc = torch.zeros(1, page, hq, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    tables = torch.zeros(1, 1, dtype=torch.int32, device="cuda")
+    lengths = torch.ones(1, dtype=torch.int32, device="cuda")
+    qs = _native.int64_array(q.stride())
+    kvs = _native.int64_array(kc.stride())
+    rc = lib.rlt_paged_decode_no_alloc(
+        q.data_ptr(), qs, kc.data_ptr(), vc.data_ptr(), kvs, tables.data_ptr(), 1, 1, lengths.data_ptr(),
+        out.data_ptr(), _native.int64_array(out.stride()), 1, hq, hq, d, page, 1, 1.0, _native.RLT_BFLOAT16,
+        torch.cuda.current_stream().cuda_stream,
+    )
+    torch.cuda.synchronize()
     assert rc == _native.RLT_EUNSUPPORTED and "static scratch" in _native.last_error()

@@ -1304,6 +1304,8 @@ int scratch_for_stream(void* stream, void** out) {
 }  // namespace
 }  // namespace rlt
 
+extern "C" int64_t rlt_static_device_bytes(void) { return kNoAllocScratchBytes; }
+
 extern "C" int64_t rlt_paged_decode_no_alloc_rows_per_launch(int64_t num_q_heads, int64_t num_kv_heads,
                                                               int64_t head_dim) {
   if (num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_q_heads % num_kv_heads) return 0;

@@ -84,6 +84,7 @@ SIGNATURES = {
         + [c_float, c_int, c_void_p],
     ),
     "rlt_paged_decode_no_alloc_rows_per_launch": (c_int64, [c_int64] * 3),
+    "rlt_static_device_bytes": (c_int64, []),
     "rlt_paged_decode_shared_prefix": (
         c_int,
         [c_void_p, _i64p, c_void_p, c_void_p, _i64p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, _i64p]

@@ -77,9 +77,23 @@ class RoutingBank:
         self.tokens = torch.empty((self.rows, 1), dtype=torch.int64, device=device)
 
     @staticmethod
-    def device_bytes(rows: int, width: int, hidden_size: int, element_size: int) -> int:
-        """Device memory one transferring bank holds (arenas, hidden and token rows)."""
-        return rows * (4 * 8 + 4 * (1 + width) + hidden_size * element_size + 8)
+    def device_bytes(rows: int, width: int, hidden_size: int, element_size: int, staging_patches: int = 0) -> int:
+        """Device memory one transferring bank holds (arenas, hidden and token rows).
+
+        staging_patches > 0 adds the device copy of the pinned buffer that a
+        bank without UVA keeps, at that patch capacity.
+        """
+        arenas = rows * (4 * 8 + 4 * (1 + width) + hidden_size * element_size + 8)
+        staging = 8 * (3 * rows + 2 * staging_patches) if staging_patches else 0
+        return arenas + staging
+
+    @staticmethod
+    def staging_capacity_bound(rows: int, max_num_seqs: int, planes: int, width: int) -> int:
+        """Largest patch capacity a bank reaches: a step ships at most every plane's
+        whole table of each of its requests, and the capacity starts at 4 x rows and
+        grows to max(need, twice the old capacity)."""
+        need = min(rows, max_num_seqs) * planes * width
+        return max(4 * rows, 2 * need)
 
     # ------------------------------------------------------------ host side
     def _alloc_host(self, patch_capacity: int) -> None:
@@ -205,10 +219,12 @@ class AsyncState:
 
     @staticmethod
     def device_bytes(max_num_seqs: int, rows: int, hidden_size: int, width: int, planes: int, element_size: int,
-                     banks: int = DEFAULT_BANKS) -> int:
-        """Device memory an AsyncState of this shape allocates."""
+                     banks: int = DEFAULT_BANKS, use_uva: bool = True) -> int:
+        """Device memory an AsyncState of this shape allocates (without UVA, each bank's
+        staging copy at its largest capacity included)."""
         pools = max_num_seqs * (hidden_size * element_size + 8 + planes * width * 4)
-        return pools + banks * RoutingBank.device_bytes(rows, width, hidden_size, element_size)
+        patches = 0 if use_uva else RoutingBank.staging_capacity_bound(rows, max_num_seqs, planes, width)
+        return pools + banks * RoutingBank.device_bytes(rows, width, hidden_size, element_size, patches)
 
     def _next_bank(self, finalize: bool) -> RoutingBank:
         if finalize:

@@ -251,6 +251,11 @@ def decode_workspace_bytes(n_rows: int, num_q_heads: int, num_kv_heads: int, hea
     return int(_native.load().rlt_paged_decode_workspace_bytes(n_rows, num_q_heads, num_kv_heads, head_dim))
 
 
+def static_device_bytes() -> int:
+    """Device bytes the library holds per device it has run on (rlt_static_device_bytes)."""
+    return int(_native.load().rlt_static_device_bytes())
+
+
 def prefill_workspace_bytes(
     total_q: int, num_seqs: int, table_width: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
     page_size: int, dtype: torch.dtype,

@@ -36,9 +36,12 @@ class HipPagedAttention:
     partials and the per-token prefill path, so steady-state calls allocate
     nothing.  It grows to the next power of two when a batch needs more
     (reserve() grows it ahead of a graph capture).  A buffer it outgrows is
-    kept alive, not freed, because a captured graph may still hold its
-    address.  Calls on one object are meant to run on one stream, in order:
-    two streams sharing the object at once would share the workspace.
+    released, unless a graph was captured while it was the workspace: such a
+    graph keeps reading that address, so the buffer stays alive with the
+    object.  Graphs captured at growing sizes therefore hold less than the
+    final workspace again (powers of two below it).  Calls on one object are
+    meant to run on one stream, in order: two streams sharing the object at
+    once would share the workspace.
     """
 
     generation = None
@@ -59,7 +62,8 @@ class HipPagedAttention:
         self.head_dim = head_dim
         self.block_size = block_size
         self._workspace = None
-        self._outgrown = []
+        self._captured = False  # a graph was captured reading the current workspace
+        self._held = []  # outgrown workspaces a captured graph still reads
         self.info = dict(
             backend="hip",
             arch="gfx950",
@@ -71,6 +75,11 @@ class HipPagedAttention:
     def workspace_bytes(self) -> int:
         return 0 if self._workspace is None else self._workspace.numel()
 
+    @property
+    def held_bytes(self) -> int:
+        """Bytes of outgrown workspaces kept alive for captured graphs."""
+        return sum(t.numel() for t in self._held)
+
     @staticmethod
     def workspace_size_for(nbytes: int) -> int:
         """Size the workspace grows to for a need of nbytes: a power of two, 1 MiB or more."""
@@ -79,10 +88,18 @@ class HipPagedAttention:
     def reserve(self, nbytes: int) -> torch.Tensor:
         """The workspace, grown to at least nbytes."""
         if self._workspace is None or self._workspace.numel() < int(nbytes):
-            if self._workspace is not None:
-                self._outgrown.append(self._workspace)
+            if self._workspace is not None and self._captured:
+                self._held.append(self._workspace)
+            elif self._workspace is not None:
+                # Back to the caching allocator, reusable only once the work
+                # queued on this stream (the object's stream) has finished.
+                self._workspace.record_stream(torch.cuda.current_stream(self.device))
+            self._workspace = None
             size = self.workspace_size_for(nbytes)
             self._workspace = torch.empty(size, dtype=torch.uint8, device=self.device)
+            self._captured = False
+        if torch.cuda.is_current_stream_capturing():
+            self._captured = True
         return self._workspace
 
     def reserve_decode(self, rows: int, num_q_heads: int, num_kv_heads: int) -> torch.Tensor:
