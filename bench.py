@@ -58,6 +58,13 @@ WORKLOADS = {
     # layers and 4 planes: launch-bound, where graph replay matters.
     "ouro-small-batch": dict(batch=4, ctx=(1, 256), planes=LOOPS, depth_probs=None, refill=False, prefix=0),
 }
+# The headline workload (the bench line) and the configs measured after it in
+# the same run, each reported under the line's `workloads` key.
+HEADLINE = "ouro-last-exited"
+SECONDARY = ("ouro-shared", "ouro-prefix-stress", "ouro-prefill")
+# CPU baseline row sampling of the large decode workloads: every n-th row,
+# scaled back to the whole batch (keeps each CPU sample to seconds).
+CPU_ROW_SAMPLE = {"ouro-shared": 4, "ouro-prefix-stress": 4}
 # SHARED refill: a request finishes after U{1..8} generated tokens.
 REFILL_TOKENS = (1, 8)
 # Chunked prefill: 8 sequences x 512 new tokens over prefixes U[0, 16384], the
@@ -72,7 +79,10 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", choices=sorted(WORKLOADS) + ["ouro-prefill"], default="ouro-last-exited")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--cpu-reps", type=int, default=3, help="timed repetitions of the CPU baseline sample")
+    p.add_argument("--cpu-reps", type=int, default=5, help="timed repetitions of each CPU baseline sample")
+    p.add_argument(
+        "--only", action="store_true", help="run only --workload (the default run adds the other configs)"
+    )
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-check", action="store_true", help="skip the pre-timing parity spot check")
     p.add_argument(
@@ -459,15 +469,28 @@ def cpu_description(threads):
     }
 
 
-def cpu_baseline(w, step, reps):
+def median_time(fn, reps):
+    """Median wall time of `reps` runs of fn() after one untimed warmup run."""
+    fn()
+    times = []
+    for _ in range(max(reps, 1)):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baseline(w, step, reps, rows_sample=None):
     """The CPU oracle (op-for-op restatement of the reference CPU path) on one loop-step.
 
-    Sample: every row of the workload at `step`.  The host metadata build of
-    the loop-step (_prepare_batch: write addresses, -1-padded tables, lengths,
+    Sample: the workload's rows at `step` (every `rows_sample`-th row when
+    given, scaled back to the batch).  The host metadata build of the loop-step
+    (_prepare_batch: write addresses, -1-padded tables, lengths,
     kv_cache_manager.py:398-478) once, then one layer-step: index_put-style KV
     append plus paged attention over a 1-layer host copy of exactly the pages
     those rows reference.  loop-steps/s = 1 / (metadata + 24 * layer-step),
-    medians, with every core the process may use.
+    medians of `reps` runs after one warmup, on every core the process may use
+    and on one thread.
     """
     from oracle import kv_ops
     from oracle.paged_attention import paged_attention_cpu
@@ -475,28 +498,25 @@ def cpu_baseline(w, step, reps):
     threads = usable_cpus()
     torch.set_num_threads(threads)
     torch.cuda.synchronize()
-    desc = w.descriptors_host[step].tolist()
+    stride = rows_sample or 1
+    picked = list(range(0, w.batch, stride))
+    scale = w.batch / len(picked)
+    desc = [w.descriptors_host[step].tolist()[r] for r in picked]
     host_tables = [tuple(w.tables_host[slot, plane].tolist()) for slot, plane, _ in desc]
     host_positions = [pos for _, _, pos in desc]
-    lengths = w.lengths.cpu()
-    tables = w.row_tables.cpu()
-    need = sorted({int(b) for r in range(w.batch) for b in tables[r, : math.ceil(int(lengths[r]) / PAGE)]})
+    sel = torch.tensor(picked)
+    lengths = w.lengths.cpu()[sel]
+    tables = w.row_tables.cpu()[sel]
+    need = sorted({int(b) for r in range(len(picked)) for b in tables[r, : math.ceil(int(lengths[r]) / PAGE)]})
     remap = torch.full((w.num_blocks,), -1, dtype=torch.int64)
     remap[torch.tensor(need)] = torch.arange(len(need))
     idx = torch.tensor(need, device=w.device)
     kc = w.key_cache[idx, 0:1].cpu()  # [used blocks, 1 layer, page, hkv, d]
     vc = w.value_cache[idx, 0:1].cpu()
     local = torch.where(tables >= 0, remap[tables.clamp_min(0).long()], -1).to(torch.int32)
-    blocks = remap[w.blocks.cpu()]
-    offsets = w.offsets.cpu()
-    q, k_new, v_new = w.q[0].cpu(), w.k_new[0].cpu(), w.v_new[0].cpu()
-    def median_time(fn, reps):
-        times = []
-        for _ in range(reps + 1):
-            t0 = time.perf_counter()
-            fn()
-            times.append(time.perf_counter() - t0)
-        return statistics.median(times[1:])
+    blocks = remap[w.blocks.cpu()[sel]]
+    offsets = w.offsets.cpu()[sel]
+    q, k_new, v_new = w.q[0].cpu()[sel], w.k_new[0].cpu()[sel], w.v_new[0].cpu()[sel]
 
     def metadata():
         b, o, t, n = kv_ops.prepare_addresses(host_tables, host_positions, PAGE)
@@ -506,12 +526,13 @@ def cpu_baseline(w, step, reps):
         kv_ops.append(kc, vc, 0, blocks, offsets, k_new, v_new)
         paged_attention_cpu(q, kc[:, 0], vc[:, 0], local, lengths)
 
-    meta_s = median_time(metadata, reps)
-    layer_s = median_time(layer, reps)
+    meta_s = median_time(metadata, reps) * scale
+    layer_s = median_time(layer, reps) * scale
     torch.set_num_threads(1)
-    single_s = median_time(layer, 1)
+    single_s = median_time(layer, reps) * scale
     torch.set_num_threads(threads)
     loop_s = meta_s + LAYERS * layer_s
+    rows_text = f"all {w.batch} rows" if stride == 1 else f"every {stride}th row ({len(picked)} of {w.batch}, x{scale:g})"
     return {
         "value": 1.0 / loop_s,
         "unit": "loop-steps/s",
@@ -519,10 +540,87 @@ def cpu_baseline(w, step, reps):
         "kind": "port",
         "single_thread_value": 1.0 / (meta_s + LAYERS * single_s),
         **cpu_description(threads),
-        "sample": f"one loop-step of all {w.batch} rows: the host metadata build ({meta_s * 1e3:.2f} ms) plus "
+        "sample": f"one loop-step of {rows_text}: the host metadata build ({meta_s * 1e3:.2f} ms) plus "
         f"one layer-step (append + attention, 1-layer pool) extrapolated x{LAYERS} layers; "
-        f"{layer_s * 1e3:.1f} ms/layer-step on {threads} threads (median of {reps} after 1 warmup), "
-        f"{single_s * 1e3:.1f} ms on 1 thread (1 run after 1 warmup)",
+        f"{layer_s * 1e3:.1f} ms/layer-step on {threads} threads, {single_s * 1e3:.1f} ms on 1 thread "
+        f"(medians of {reps} after 1 warmup)",
+    }
+
+
+def config1_exact(seed, device, reps):
+    """The reference CPU case timed exactly: batch 4, 16/16 heads, head_dim 128, page 16,
+    contexts U[1, 256], one layer, one depth, one appended token per sequence, then
+    decode attention.  CPU: host metadata + index_put append + the oracle's
+    attention; GPU: the fused append + decode launch on the same inputs (events
+    around 100 launches).  Microseconds per step, medians."""
+    from oracle import kv_ops
+    from oracle.paged_attention import paged_attention_cpu
+    from vllm_rlt_amd import ops
+
+    g = torch.Generator().manual_seed(seed)
+    rows = 4
+    contexts = torch.randint(1, 257, (rows,), generator=g)
+    pages = [(int(c) + 1 + PAGE - 1) // PAGE for c in contexts]
+    nb = sum(pages) + 2
+    perm = torch.randperm(nb, generator=g)
+    tables = torch.full((rows, max(pages)), -1, dtype=torch.int32)
+    used = 0
+    for r, n in enumerate(pages):
+        tables[r, :n] = perm[used : used + n].to(torch.int32)
+        used += n
+    kc = torch.randn(nb, 1, PAGE, HKV, HEAD_DIM, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, 1, PAGE, HKV, HEAD_DIM, generator=g).to(torch.bfloat16)
+    q = torch.randn(rows, HQ, HEAD_DIM, generator=g).to(torch.bfloat16)
+    k_new = torch.randn(rows, HKV, HEAD_DIM, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(rows, HKV, HEAD_DIM, generator=g).to(torch.bfloat16)
+    table_rows = [tuple(int(x) for x in tables[r, : pages[r]]) for r in range(rows)]
+    positions = [int(c) for c in contexts]
+
+    def cpu_step():
+        b, o, t, n = kv_ops.prepare_addresses(table_rows, positions, PAGE)
+        kv_ops.append(kc, vc, 0, torch.from_numpy(b), torch.from_numpy(o), k_new, v_new)
+        return paged_attention_cpu(q, kc[:, 0], vc[:, 0], torch.from_numpy(t), torch.from_numpy(n))
+
+    threads = usable_cpus()
+    torch.set_num_threads(threads)
+    cpu_s = median_time(cpu_step, reps)
+    torch.set_num_threads(1)
+    single_s = median_time(cpu_step, reps)
+    torch.set_num_threads(threads)
+    expect = cpu_step()
+    # GPU: same inputs; appending the same token again rewrites the same bits.
+    b, o, t, n = (torch.from_numpy(x).to(device) for x in kv_ops.prepare_addresses(table_rows, positions, PAGE))
+    dk, dv = kc.to(device), vc.to(device)
+    dq, dkn, dvn = q.to(device), k_new.to(device), v_new.to(device)
+    out = torch.empty_like(dq)
+    ws = torch.empty(ops.decode_workspace_bytes(rows, HQ, HKV, HEAD_DIM), dtype=torch.uint8, device=device)
+
+    def gpu_step():
+        ops.paged_decode_append(dq, dk[:, 0], dv[:, 0], t, n, dkn, dvn, b, o, out=out, workspace=ws)
+
+    gpu_step()
+    torch.cuda.synchronize()
+    if not torch.allclose(out.cpu().float(), expect.float(), atol=2e-2, rtol=1e-2):
+        raise SystemExit("config-1 parity check failed")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(100):
+        gpu_step()
+    end.record()
+    torch.cuda.synchronize()
+    gpu_us = start.elapsed_time(end) * 10.0
+    lengths = [p + 1 for p in positions]
+    step_bytes_1 = sum(2 * HKV * HEAD_DIM * 2 * n + 4 * HQ * HEAD_DIM * 2 + 4 * HKV * HEAD_DIM * 2 for n in lengths)
+    return {
+        "workload": "batch 4, 16/16 heads, head_dim 128, page 16, bf16, contexts U[1,256] "
+        f"({positions}), 1 layer, 1 depth: append 1 token per sequence, then decode attention",
+        "cpu_us_per_step": round(cpu_s * 1e6, 1),
+        "cpu_single_thread_us_per_step": round(single_s * 1e6, 1),
+        "cpu_threads": threads,
+        "gpu_us_per_step": round(gpu_us, 2),
+        "algorithmic_bytes_per_step": step_bytes_1,
+        "gpu_gb_per_s": round(step_bytes_1 / (gpu_us * 1e-6) / 1e9, 1),
+        "reps": f"CPU medians of {reps} after 1 warmup; GPU mean of 100 launches between two events",
     }
 
 
@@ -652,17 +750,12 @@ def prefill_cpu_baseline(w, reps, stride=32):
     q = w.q[0][rows].cpu()
     lengths = torch.tensor(row_lens, dtype=torch.int32)
 
-    def timed(reps):
-        times = []
-        for _ in range(reps + 1):
-            t0 = time.perf_counter()
-            paged_attention_cpu(q, kc, vc, local, lengths)
-            times.append(time.perf_counter() - t0)
-        return statistics.median(times[1:])
+    def attend():
+        paged_attention_cpu(q, kc, vc, local, lengths)
 
-    t_multi = timed(reps)
+    t_multi = median_time(attend, reps)
     torch.set_num_threads(1)
-    t_single = timed(1)
+    t_single = median_time(attend, reps)
     torch.set_num_threads(threads)
     flops = 4 * HQ * HEAD_DIM * sum(row_lens)
     return {
@@ -673,7 +766,7 @@ def prefill_cpu_baseline(w, reps, stride=32):
         "single_thread_value": flops / t_single / 1e12,
         **cpu_description(threads),
         "sample": f"{len(rows)} query rows (1 in {stride} of each 512-token chunk, depth 0, layer 0, "
-        f"{sum(row_lens)} visible keys), median of {reps} after 1 warmup: {t_multi * 1e3:.1f} ms on {threads} "
+        f"{sum(row_lens)} visible keys), medians of {reps} after 1 warmup: {t_multi * 1e3:.1f} ms on {threads} "
         f"threads, {t_single * 1e3:.1f} ms on 1 thread",
     }
 
@@ -689,11 +782,12 @@ def run_prefill(args, device):
         file=sys.stderr,
         flush=True,
     )
+    err = None
     for step in range(args.warmup):
         w.step()
         if step == 0 and not args.no_check:
             err = prefill_spot_check(w)
-            print(f"[bench] prefill parity spot check ok (max-abs {err:.3g})", file=sys.stderr, flush=True)
+            print(f"[bench] ouro-prefill: parity spot check ok (max-abs {err:.3g})", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -729,6 +823,7 @@ def run_prefill(args, device):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
+        "parity_max_abs": err,
         "config": {
             "workload": f"ouro-prefill: {PREFILL['seqs']} sequences x {PREFILL['chunk']} new tokens over prefixes "
             f"U{list(PREFILL['prefix'])}, 16/16 heads, head_dim 128, page 16, LAST-EXITED, step = 4 depths x 24 "
@@ -753,9 +848,188 @@ def run_prefill(args, device):
         },
     }
     if not args.no_cpu_baseline:
-        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        print("[bench] ouro-prefill: timing the CPU oracle baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = prefill_cpu_baseline(w, args.cpu_reps)
-    print(json.dumps(line), flush=True)
+    release(w)
+    return line
+
+
+def release(*objects):
+    """Drop a workload's device memory before the next one is set up."""
+    for obj in objects:
+        del obj
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def run_decode(args, name, device, with_cpu=True):
+    """One decode workload: timed loop-steps, the per-step launch window, parity, CPU baseline."""
+    total = args.warmup + args.steps
+    t_setup = time.perf_counter()
+    w = Workload(name, total, args.seed, device)
+    w.fused_append = args.append == "fused" and w.prefix_hint is None
+    torch.cuda.synchronize()
+    print(
+        f"[bench] workload {name}: batch {w.batch}, planes {w.planes}, pool "
+        f"{w.pool_bytes() / 1e9:.1f} GB ({w.num_blocks} pages), setup {time.perf_counter() - t_setup:.1f}s",
+        file=sys.stderr,
+        flush=True,
+    )
+
+    snapshot = w.shared_snapshot()
+    # Warmup (also the parity spot check on step 0).
+    spot = None
+    for step in range(args.warmup):
+        loop_step(w, step)
+        if step == 0 and not args.no_check:
+            spot = spot_check(w)
+            print(f"[bench] {name}: parity spot check ok (max-abs {spot:.3g})", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` loop-steps.
+    total_bytes = 0
+    decode_bytes, unique_bytes = [], []
+    for step in range(args.warmup, total):
+        b, d, u = step_bytes(w.lengths_at(step), w.prefix_tokens)
+        total_bytes += b
+        decode_bytes.append(d)
+        unique_bytes.append(u)
+    graph = None
+    if args.graph:
+        graph, static = capture_loop_step(w)
+        for step in range(args.warmup):  # warm the replay path too
+            static.copy_(w.descriptors[step])
+            graph.replay()
+    torch.cuda.synchronize()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    # Eager steps also mark the end of their metadata build: the window from
+    # there to the step's end holds exactly its 24 layer launches.
+    launched = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    marks[0].record()
+    if graph is None:
+        for i, step in enumerate(range(args.warmup, total)):
+            build_metadata(w, step)
+            launched[i].record()
+            for layer in range(LAYERS):
+                layer_step(w, layer)
+            marks[i + 1].record()
+    else:
+        for i, step in enumerate(range(args.warmup, total)):
+            static.copy_(w.descriptors[step])
+            graph.replay()
+            marks[i + 1].record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    step_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
+    if graph is not None:
+        # The replayed steps must leave the same outputs as eager steps.
+        last = w.out.clone()
+        loop_step(w, total - 1)
+        torch.cuda.synchronize()
+        if not torch.equal(last.view(torch.int16), w.out.view(torch.int16)):
+            raise SystemExit("graph replay differs from eager execution")
+
+    # Launch timing, from the timed steps themselves (all work is on the
+    # current stream): a launch's time is its step's launch window / 24, gaps
+    # between launches included, so 24 launches never add up to more than a
+    # step.  No event sits between two launches of a window.  Graph replays
+    # have no such mark; their step window (metadata build included) is used.
+    if graph is None:
+        windows = [launched[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
+    else:
+        windows = step_ms
+    launch_ms = [t / LAYERS for t in windows]
+    decode_ms = statistics.fmean(launch_ms)
+    # The fused launch also moves the new tokens: 8 KiB read + 8 KiB written + 16 B of address per row;
+    # with a separate append launch, the window holds the append too.
+    append_bytes = w.batch * (4 * HKV * HEAD_DIM * 2 + 16)
+    decode_avg_bytes = statistics.fmean(decode_bytes) + append_bytes
+    unique_avg_bytes = statistics.fmean(unique_bytes) + append_bytes
+    # Aliased prefix pages are read by every row but fetched from HBM about
+    # once per launch: the roofline uses the unique bytes.
+    achieved = unique_avg_bytes / (decode_ms * 1e-3) / 1e9
+    if snapshot is not None:
+        if not w.shared_unchanged(snapshot):
+            raise SystemExit("aliased prefix pages changed during the run")
+        print(f"[bench] {name}: aliased prefix pages unchanged (bitwise)", file=sys.stderr, flush=True)
+        del snapshot
+
+    steps_per_s = args.steps / elapsed
+    gbs = total_bytes / elapsed / 1e9
+    if w.fused_append:
+        kernel = (
+            "rlt_paged_decode_append (paged_decode_kernel split pass reading each row's new token in place + "
+            "paged_decode_merge_kernel storing it)"
+        )
+    elif w.prefix_hint is None:
+        kernel = "rlt_kv_append + rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
+    else:
+        kernel = (
+            "rlt_kv_append + rlt_paged_decode_shared_prefix (shared_prefix_kernel + paged_decode_kernel split "
+            "pass + paged_decode_merge_kernel)"
+        )
+    line = {
+        "metric": "paged decode attn+KV append: HBM GB/s (% peak), loop-steps/s at Ouro-1.4B",
+        "value": round(steps_per_s, 3),
+        "unit": "loop-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": describe(name),
+            "global_batch": w.batch,
+            "seq_len": int(w.contexts.float().mean().item()),
+            "parallelism": "single-gpu",
+            "launch": "hip-graph replay" if graph is not None else "eager",
+            "append": "fused into the decode launch" if w.fused_append else "own launch before the decode",
+        },
+        "hbm_gb_per_s": round(gbs, 1),
+        "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "step_ms_median": round(statistics.median(step_ms), 4),
+        "step_ms_iqr": iqr(step_ms),
+        "parity_max_abs": spot,
+        "roofline": {
+            "kernel": kernel,
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": profiled_traffic(name),
+            "rocprof_avg_launch_ms": profiled_launch_ms(name),
+            "avg_launch_ms": round(decode_ms, 5),
+            "median_launch_ms": round(statistics.median(launch_ms), 5),
+            "launch_ms_iqr": iqr(launch_ms),
+            "launch_timing": "timed loop-steps: event after the metadata build to the step's end event, / 24 "
+            "(gaps between launches included)",
+            "algorithmic_bytes_per_launch": int(unique_avg_bytes),
+        },
+    }
+    if w.prefix_tokens:
+        line["roofline"]["per_request_bytes_per_launch"] = int(decode_avg_bytes)
+        line["roofline"]["per_request_gb_per_s"] = round(decode_avg_bytes / (decode_ms * 1e-3) / 1e9, 1)
+    if with_cpu and not args.no_cpu_baseline:
+        print(f"[bench] {name}: timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(w, total - 1, args.cpu_reps, rows_sample=CPU_ROW_SAMPLE.get(name))
+    release(w)
+    return line
+
+
+def compact(line):
+    """A secondary workload's figures for the headline line's `workloads` key."""
+    keep = ("metric", "value", "unit", "ms_per_step", "steps", "warmup", "hbm_gb_per_s", "hbm_frac_of_peak",
+            "step_ms_median", "step_ms_iqr", "parity_max_abs", "config", "roofline", "cpu_baseline")
+    return {k: line[k] for k in keep if k in line}
 
 
 def main():
@@ -782,164 +1056,19 @@ def main():
         calibrate_counters(device)
         return
     if args.workload == "ouro-prefill":
-        run_prefill(args, device)
+        print(json.dumps(run_prefill(args, device)), flush=True)
         return
-    total = args.warmup + args.steps
-    t_setup = time.perf_counter()
-    w = Workload(args.workload, total, args.seed, device)
-    w.fused_append = args.append == "fused" and w.prefix_hint is None
-    torch.cuda.synchronize()
-    print(
-        f"[bench] workload {args.workload}: batch {w.batch}, planes {w.planes}, pool "
-        f"{w.pool_bytes() / 1e9:.1f} GB ({w.num_blocks} pages), setup {time.perf_counter() - t_setup:.1f}s",
-        file=sys.stderr,
-        flush=True,
-    )
-
-    snapshot = w.shared_snapshot()
-    # Warmup (also the parity spot check on step 0).
-    for step in range(args.warmup):
-        loop_step(w, step)
-        if step == 0 and not args.no_check:
-            err = spot_check(w)
-            print(f"[bench] parity spot check ok (max-abs {err:.3g})", file=sys.stderr, flush=True)
-    torch.cuda.synchronize()
-
-    # Timed region: exactly `steps` loop-steps.
-    total_bytes = 0
-    decode_bytes, unique_bytes = [], []
-    for step in range(args.warmup, total):
-        b, d, u = step_bytes(w.lengths_at(step), w.prefix_tokens)
-        total_bytes += b
-        decode_bytes.append(d)
-        unique_bytes.append(u)
-    graph = None
-    if args.graph:
-        graph, static = capture_loop_step(w)
-        for step in range(args.warmup):  # warm the replay path too
-            static.copy_(w.descriptors[step])
-            graph.replay()
-    torch.cuda.synchronize()
-    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    t0 = time.perf_counter()
-    marks[0].record()
-    if graph is None:
-        for i, step in enumerate(range(args.warmup, total)):
-            loop_step(w, step)
-            marks[i + 1].record()
-    else:
-        for i, step in enumerate(range(args.warmup, total)):
-            static.copy_(w.descriptors[step])
-            graph.replay()
-            marks[i + 1].record()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    step_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
-    if graph is not None:
-        # The replayed steps must leave the same outputs as eager steps.
-        last = w.out.clone()
-        loop_step(w, total - 1)
-        torch.cuda.synchronize()
-        if not torch.equal(last.view(torch.int16), w.out.view(torch.int16)):
-            raise SystemExit("graph replay differs from eager execution")
-
-    # Decode-launch timing with HIP events on the launch stream (separate pass,
-    # same steps): each event pair brackets one decode launch, the fused
-    # append-and-decode one when the loop-step uses it.
-    from vllm_rlt_amd import ops
-
-    stream = torch.cuda.current_stream(device)
-    # Events are created before the pass, so no event creation sits between launches.
-    pairs = [
-        (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        for _ in range((total - args.warmup) * LAYERS)
-    ]
-    events = iter(pairs)
-    for step in range(args.warmup, total):
-        build_metadata(w, step)
-        for layer in range(LAYERS):
-            if not w.fused_append:
-                ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
-            start, end = next(events)
-            start.record(stream)
-            if w.fused_append:
-                layer_step(w, layer)
-            else:
-                ops.paged_decode(
-                    w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths,
-                    out=w.out[layer], workspace=w.workspace, shared_prefix=w.prefix_hint,
-                )
-            end.record(stream)
-    torch.cuda.synchronize()
-    launch_ms = [s.elapsed_time(e) for s, e in pairs]
-    decode_ms = statistics.fmean(launch_ms)
-    # The fused launch also moves the new tokens: 8 KiB read + 8 KiB written + 16 B of address per row.
-    fused_extra = w.batch * (4 * HKV * HEAD_DIM * 2 + 16) if w.fused_append else 0
-    decode_avg_bytes = statistics.fmean(decode_bytes) + fused_extra
-    unique_avg_bytes = statistics.fmean(unique_bytes) + fused_extra
-    # Aliased prefix pages are read by every row but fetched from HBM about
-    # once per launch: the roofline uses the unique bytes.
-    achieved = unique_avg_bytes / (decode_ms * 1e-3) / 1e9
-    if snapshot is not None:
-        if not w.shared_unchanged(snapshot):
-            raise SystemExit("aliased prefix pages changed during the run")
-        print("[bench] aliased prefix pages unchanged (bitwise)", file=sys.stderr, flush=True)
-        del snapshot
-
-    steps_per_s = args.steps / elapsed
-    gbs = total_bytes / elapsed / 1e9
-    line = {
-        "metric": "paged decode attn+KV append: HBM GB/s (% peak), loop-steps/s at Ouro-1.4B",
-        "value": round(steps_per_s, 3),
-        "unit": "loop-steps/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": describe(args.workload),
-            "global_batch": w.batch,
-            "seq_len": int(w.contexts.float().mean().item()),
-            "parallelism": "single-gpu",
-            "launch": "hip-graph replay" if graph is not None else "eager",
-            "append": "fused into the decode launch" if w.fused_append else "own launch before the decode",
-        },
-        "hbm_gb_per_s": round(gbs, 1),
-        "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
-        "step_ms_median": round(statistics.median(step_ms), 4),
-        "step_ms_iqr": iqr(step_ms),
-        "roofline": {
-            "kernel": "rlt_paged_decode_append (paged_decode_kernel split pass reading each row's new token "
-            "in place + paged_decode_merge_kernel storing it)"
-            if w.fused_append
-            else "rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
-            if w.prefix_hint is None
-            else "rlt_paged_decode_shared_prefix (shared_prefix_kernel + paged_decode_kernel split pass + "
-            "paged_decode_merge_kernel)",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(args.workload),
-            "rocprof_avg_launch_ms": profiled_launch_ms(args.workload),
-            "avg_launch_ms": round(decode_ms, 5),
-            "median_launch_ms": round(statistics.median(launch_ms), 5),
-            "launch_ms_iqr": iqr(launch_ms),
-            "algorithmic_bytes_per_launch": int(unique_avg_bytes),
-        },
-    }
-    if w.prefix_tokens:
-        line["roofline"]["per_request_bytes_per_launch"] = int(decode_avg_bytes)
-        line["roofline"]["per_request_gb_per_s"] = round(decode_avg_bytes / (decode_ms * 1e-3) / 1e9, 1)
-    if not args.no_cpu_baseline:
-        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(w, total - 1, args.cpu_reps)
+    line = run_decode(args, args.workload, device)
+    if args.workload == HEADLINE and not args.only:
+        # The other measured configs, each after the previous pool is freed.
+        extra = {}
+        for name in SECONDARY:
+            t0 = time.perf_counter()
+            extra[name] = compact(run_prefill(args, device) if name == "ouro-prefill" else run_decode(args, name, device))
+            print(f"[bench] {name} done in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+        line["workloads"] = extra
+        if not args.no_cpu_baseline and "cpu_baseline" in line:
+            line["cpu_baseline"]["config1_exact"] = config1_exact(args.seed, device, args.cpu_reps)
     print(json.dumps(line), flush=True)
 
 
