@@ -54,6 +54,13 @@ WORKLOADS = {
     "ouro-prefix-stress": dict(
         batch=64, ctx=(16384, 32768), planes=1, depth_probs=None, refill=False, prefix=8192
     ),
+    # Prefix caching under the reference's own semantics (LAST-EXITED only,
+    # a published prefix holds one page per plane): 4 planes, each with its
+    # own 2048-token prefix aliased by every row at that depth; contexts are
+    # the prefix-stress ones scaled by 1/4 so the 4 planes fit one GPU.
+    "ouro-prefix-last-exited": dict(
+        batch=64, ctx=(4096, 8192), planes=LOOPS, depth_probs=None, refill=False, prefix=2048
+    ),
     # The reference CPU case's shape (batch 4, contexts U[1, 256]) over all 24
     # layers and 4 planes: launch-bound, where graph replay matters.
     "ouro-small-batch": dict(batch=4, ctx=(1, 256), planes=LOOPS, depth_probs=None, refill=False, prefix=0),
@@ -61,10 +68,10 @@ WORKLOADS = {
 # The headline workload (the bench line) and the configs measured after it in
 # the same run, each reported under the line's `workloads` key.
 HEADLINE = "ouro-last-exited"
-SECONDARY = ("ouro-shared", "ouro-prefix-stress", "ouro-prefill")
+SECONDARY = ("ouro-shared", "ouro-prefix-stress", "ouro-prefix-last-exited", "ouro-prefill")
 # CPU baseline row sampling of the large decode workloads: every n-th row,
 # scaled back to the whole batch (keeps each CPU sample to seconds).
-CPU_ROW_SAMPLE = {"ouro-shared": 4, "ouro-prefix-stress": 4}
+CPU_ROW_SAMPLE = {"ouro-shared": 4, "ouro-prefix-stress": 4, "ouro-prefix-last-exited": 2}
 # SHARED refill: a request finishes after U{1..8} generated tokens.
 REFILL_TOKENS = (1, 8)
 # Chunked prefill: 8 sequences x 512 new tokens over prefixes U[0, 16384], the
@@ -163,7 +170,8 @@ def describe(name):
     elif cfg["planes"] > 1:
         text += ", each step every request at a depth drawn from U{1..4}"
     if cfg["prefix"]:
-        text += f", a {cfg['prefix']}-token prefix aliased read-only in every table"
+        where = "every table" if cfg["planes"] == 1 else "every plane's table (one prefix per plane)"
+        text += f", a {cfg['prefix']}-token prefix aliased read-only in {where}"
     return text + "; loop-step = metadata build + 24 x (KV append + decode)"
 
 
@@ -171,9 +179,10 @@ def make_schedule(name, total_steps, seed):
     """Host-side page tables and per-step (slot, plane, position) descriptors of a decode workload.
 
     Returns (descriptors [steps, batch, 3] int64, tables [slots, planes, width]
-    int32, num_blocks, contexts, shared_pages).  Without refill, every request
-    keeps one slot, appends at context + step, and its table covers every
-    position the run touches.  With refill (SHARED), a request runs loops
+    int32, num_blocks, contexts, shared_pages [planes, prefix pages]).  Without
+    refill, every request keeps one slot, appends at context + step, and its
+    table covers every position the run touches; with a prefix, each plane's
+    table begins with that plane's prefix pages.  With refill (SHARED), a request runs loops
     0 .. exit-1 on one position, then moves to the next; after its generated
     tokens it leaves, its pages return to the free list, and a new request
     with a fresh context takes a new slot, drawing pages at random positions
@@ -191,14 +200,14 @@ def make_schedule(name, total_steps, seed):
         pages = (contexts + total_steps + PAGE - 1) // PAGE
         width = int(pages.max())
         own = [int(n) - prefix_pages for n in pages]
-        num_blocks = prefix_pages + sum(own) * planes
+        num_blocks = (prefix_pages + sum(own)) * planes
         perm = torch.randperm(num_blocks, generator=g).to(torch.int32)
-        shared = perm[:prefix_pages]
-        used = prefix_pages
+        shared = perm[: prefix_pages * planes].view(planes, prefix_pages)
+        used = prefix_pages * planes
         tables = torch.zeros(batch, planes, width, dtype=torch.int32)
         for r in range(batch):
             for plane in range(planes):
-                tables[r, plane, :prefix_pages] = shared
+                tables[r, plane, :prefix_pages] = shared[plane]
                 tables[r, plane, prefix_pages : prefix_pages + own[r]] = perm[used : used + own[r]]
                 used += own[r]
         if cfg["depth_probs"] is None:
@@ -267,7 +276,7 @@ def make_schedule(name, total_steps, seed):
     tables = torch.zeros(len(slot_pages), 1, width, dtype=torch.int32)
     for slot, pg in enumerate(slot_pages):
         tables[slot, 0, : len(pg)] = torch.tensor(pg, dtype=torch.int32)
-    return desc, tables, num_blocks, contexts, torch.empty(0, dtype=torch.int64)
+    return desc, tables, num_blocks, contexts, torch.empty(1, 0, dtype=torch.int64)
 
 
 class Workload:
@@ -314,14 +323,22 @@ class Workload:
         self.workspace = torch.empty(
             ops.decode_workspace_bytes(n, HQ, HKV, HEAD_DIM), dtype=torch.uint8, device=device
         )
-        # Every row's table begins with the aliased prefix pages: the decode reads
-        # them once per launch for all rows (rlt_paged_decode_shared_prefix).
-        self.fused_append = True  # KV append inside the decode launch (no shared-prefix hint)
-        self.prefix_hint = None
+        # Every row's table begins with its plane's aliased prefix pages: the
+        # decode reads each plane's once per launch for all rows at that plane
+        # (rlt_paged_decode_shared_prefix).  The step's prefix groups follow the
+        # rows' depths; like the descriptors they are built before timing and
+        # live on the device.
+        self.fused_append = True  # KV append inside the decode launch
+        self.prefix_hints = None
         if self.shared_pages.numel():
-            self.prefix_hint = ops.shared_prefix(
-                range(n), self.shared_pages, n, [int(c) for c in self.contexts], device
-            )
+            self.prefix_hints = []
+            for step in range(total_steps):
+                planes_now = desc[step, :, 1].tolist()
+                rows_pages = [tables[r, p, : self.shared_pages.shape[1]].tolist() for r, p in enumerate(planes_now)]
+                self.prefix_hints.append(
+                    ops.prefix_groups(rows_pages, self.lengths_at(step), PAGE, HQ // HKV, device)
+                )
+        self.prefix_hint = None  # the current step's groups
 
     def lengths_at(self, step):
         """Attention length of every row at a step (context incl. the appended token)."""
@@ -331,20 +348,26 @@ class Workload:
         return 2 * self.key_cache.numel() * self.key_cache.element_size()
 
     def shared_snapshot(self):
-        """Copies of the aliased prefix pages (all layers), to prove they stay read-only."""
+        """Copies of every plane's aliased prefix pages (all layers), to prove they stay read-only."""
         if self.shared_pages.numel() == 0:
             return None
-        idx = self.shared_pages.to(self.device)
+        idx = self.shared_pages.reshape(-1).to(self.device)
         return self.key_cache[idx].clone(), self.value_cache[idx].clone()
 
     def shared_unchanged(self, snapshot):
-        idx = self.shared_pages.to(self.device)
+        idx = self.shared_pages.reshape(-1).to(self.device)
         return torch.equal(self.key_cache[idx], snapshot[0]) and torch.equal(self.value_cache[idx], snapshot[1])
+
+    def rows_per_plane(self, step):
+        """Rows of each storage plane at a step."""
+        return torch.bincount(self.descriptors_host[step, :, 1], minlength=self.planes).tolist()
 
 
 def build_metadata(w, step, descriptors=None):
     from vllm_rlt_amd import ops
 
+    if w.prefix_hints is not None:
+        w.prefix_hint = w.prefix_hints[step]
     ops.build_decode_metadata(
         w.descriptors[step] if descriptors is None else descriptors, w.batch, w.batch, w.tables, PAGE, w.slots,
         w.positions, w.lengths, w.blocks, w.offsets, w.row_tables, w.width,
@@ -355,15 +378,16 @@ def layer_step(w, layer):
     """KV append then decode attention of one layer.
 
     Every row is a different request (or a request at one depth), so no row
-    reads a slot another row writes: one fused launch unless the batch carries
-    the shared-prefix hint, which the fused launch does not take.
+    reads a slot another row writes: one fused launch (with the step's prefix
+    groups when the tables alias prefix pages).
     """
     from vllm_rlt_amd import ops
 
-    if w.prefix_hint is None and w.fused_append:
+    if w.fused_append:
         ops.paged_decode_append(
             w.q[layer], w.key_cache[:, layer], w.value_cache[:, layer], w.row_tables, w.lengths, w.k_new[layer],
             w.v_new[layer], w.blocks, w.offsets, out=w.out[layer], workspace=w.workspace,
+            shared_prefix=w.prefix_hint,
         )
         return
     ops.kv_append(w.key_cache, w.value_cache, layer, w.blocks, w.offsets, w.k_new[layer], w.v_new[layer])
@@ -390,20 +414,23 @@ def capture_loop_step(w):
     return graph, static
 
 
-def step_bytes(lengths, shared_tokens=0):
+def step_bytes(lengths, shared_tokens=0, plane_rows=None):
     """Algorithmic HBM bytes of one loop-step (24 layer-steps) and of one decode launch.
 
     Returns (loop-step bytes, decode-launch bytes, decode-launch unique bytes):
     the unique figure counts the K/V of `shared_tokens` aliased prefix tokens
-    once per launch instead of once per row that reads them, and so does the
-    loop-step figure (the decode reads the shared pages once per launch).
+    once per launch and plane instead of once per row that reads them, and so
+    does the loop-step figure (the decode reads each plane's shared pages once
+    per launch).  plane_rows: rows at each plane (default: all at one).
     """
     kv_token = 2 * HKV * HEAD_DIM * 2  # K+V of one token in one layer (8 KiB)
     qo = 2 * HQ * HEAD_DIM * 2  # q read + out write
     new_kv = 2 * HKV * HEAD_DIM * 2
     decode = sum(kv_token * n + qo + 4 * math.ceil(n / PAGE) + 4 for n in lengths)
     append = len(lengths) * (2 * new_kv + 16)  # read new k/v, write the page slots, block+offset
-    unique = decode - kv_token * shared_tokens * (len(lengths) - 1) if shared_tokens else decode
+    plane_rows = [len(lengths)] if plane_rows is None else plane_rows
+    repeats = sum(n - 1 for n in plane_rows if n > 0)
+    unique = decode - kv_token * shared_tokens * repeats
     return LAYERS * (unique + append), decode, unique
 
 
@@ -870,7 +897,7 @@ def run_decode(args, name, device, with_cpu=True):
     total = args.warmup + args.steps
     t_setup = time.perf_counter()
     w = Workload(name, total, args.seed, device)
-    w.fused_append = args.append == "fused" and w.prefix_hint is None
+    w.fused_append = args.append == "fused"
     torch.cuda.synchronize()
     print(
         f"[bench] workload {name}: batch {w.batch}, planes {w.planes}, pool "
@@ -893,12 +920,14 @@ def run_decode(args, name, device, with_cpu=True):
     total_bytes = 0
     decode_bytes, unique_bytes = [], []
     for step in range(args.warmup, total):
-        b, d, u = step_bytes(w.lengths_at(step), w.prefix_tokens)
+        b, d, u = step_bytes(w.lengths_at(step), w.prefix_tokens, w.rows_per_plane(step))
         total_bytes += b
         decode_bytes.append(d)
         unique_bytes.append(u)
     graph = None
     if args.graph:
+        if w.prefix_hints is not None:
+            raise SystemExit("--graph replays one step's metadata; the prefix workloads change their groups per step")
         graph, static = capture_loop_step(w)
         for step in range(args.warmup):  # warm the replay path too
             static.copy_(w.descriptors[step])
@@ -960,12 +989,19 @@ def run_decode(args, name, device, with_cpu=True):
 
     steps_per_s = args.steps / elapsed
     gbs = total_bytes / elapsed / 1e9
-    if w.fused_append:
+    prefix = w.prefix_hints is not None
+    if w.fused_append and prefix:
+        kernel = (
+            "rlt_paged_decode_shared_prefix with its append (shared_prefix_kernel over every plane's prefix + "
+            "paged_decode_kernel split pass reading each row's new token in place + paged_decode_merge_kernel "
+            "storing it)"
+        )
+    elif w.fused_append:
         kernel = (
             "rlt_paged_decode_append (paged_decode_kernel split pass reading each row's new token in place + "
             "paged_decode_merge_kernel storing it)"
         )
-    elif w.prefix_hint is None:
+    elif not prefix:
         kernel = "rlt_kv_append + rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
     else:
         kernel = (

@@ -280,35 +280,51 @@ int64_t rlt_paged_decode_no_alloc_rows_per_launch(int64_t num_q_heads, int64_t n
                                                   int64_t head_dim);
 
 /*
- * rlt_paged_decode for a batch whose listed rows alias one prefix (prefix-cache
- * pages shared read-only, vllm_rlt/core/kv_cache_manager.py:240-293).  Same
- * contract and result as rlt_paged_decode, which it replaces for such a batch;
- * the reference reads the shared pages once per row, this reads them once per
- * launch.
- *   prefix_member: device int32 [n_rows], nonzero for rows whose first
- *     prefix_pages table entries are prefix_table (device int32
- *     [prefix_pages]).  prefix_rows: device int32 [n_prefix_rows], exactly
- *     those rows, any order.
- *   prefix_split_len: 256 << k; the prefix pass serves the split-K splits of
- *     member rows whose split length (a function of their length alone) it is.
- * The shared splits of member rows are computed once for all of them (bf16 or
- * fp16, head_dim 128, q heads per KV head 1/2/4/8, page 16) and merged with
- * each row's remaining splits.  A split is taken from the prefix pass only if
- * the row's table entries for it equal prefix_table's, so an inexact hint
- * costs speed, not correctness; other shapes ignore the hint.  Rows must not be
- * more than 8192.
+ * rlt_paged_decode (with the append of rlt_paged_decode_append when n_write
+ * > 0) for a batch whose rows alias prefix-cache pages (shared read-only,
+ * vllm_rlt/core/kv_cache_manager.py:211-293: under LAST-EXITED every plane
+ * has its own prefix pages, so a mixed-depth batch has one aliasing group per
+ * plane and per distinct prefix).  Same contract and result as
+ * rlt_paged_decode / rlt_paged_decode_append, which it replaces for such a
+ * batch; the reference reads shared pages once per row, this reads each
+ * group's pages once per launch.
+ *   prefix_groups: device int32 buffer, in order:
+ *     row_group[n_rows]           group of each row, -1 for none;
+ *     groups[n_groups][5]         (first member index, member count, first
+ *                                  page index, page count, split length);
+ *     item_start[n_groups + 1]    prefix sums of the prefix pass's work items,
+ *                                  items of group g = min(page count x page /
+ *                                  split length, 63) x ceil(members x G / 64);
+ *     members[n_members]          the rows of every group, group after group;
+ *     pages[n_pages]              the shared page ids of every group.
+ *   n_items = item_start[n_groups].  The members of group g must be exactly
+ *   the rows with row_group == g; the split length is the decode split plan's
+ *   for the members (256 << k: a function of a row's length alone).
+ * A member's splits inside its group's pages are computed once for all
+ * members (bf16 or fp16, head_dim 128, q heads per KV head 1/2/4/8, page 16;
+ * other shapes ignore the hint) and merged with each row's remaining splits.
+ * A split is taken from the prefix pass only if the row uses the group's split
+ * length, the split is not the row's last, and the row's table entries for it
+ * equal the group's pages, so an inexact page list costs speed, not
+ * correctness.  A row's result depends on its own q, pages and group only, not
+ * on the rest of the batch.  Every index in the buffer is bounds-checked on
+ * the device: out-of-range groups, members and pages are ignored.  Rows must
+ * not be more than 8192.
  */
-int rlt_paged_decode_shared_prefix(const void* q, const int64_t* q_strides, const void* key_cache,
-                                   const void* value_cache, const int64_t* kv_strides,
+int rlt_paged_decode_shared_prefix(const void* q, const int64_t* q_strides, void* key_cache,
+                                   void* value_cache, const int64_t* kv_strides,
                                    const int32_t* block_tables, int64_t table_stride,
                                    int64_t max_table_width, const int32_t* context_lengths,
                                    void* out, const int64_t* out_strides, int64_t n_rows,
                                    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                                    int64_t page_size, int64_t num_blocks, float scale, int dtype,
-                                   void* workspace, int64_t workspace_bytes,
-                                   const int32_t* prefix_member, const int32_t* prefix_rows,
-                                   int64_t n_prefix_rows, const int32_t* prefix_table,
-                                   int64_t prefix_pages, int64_t prefix_split_len, void* stream);
+                                   const void* k_new, const int64_t* k_new_strides,
+                                   const void* v_new, const int64_t* v_new_strides,
+                                   const int64_t* write_blocks, const int64_t* write_offsets,
+                                   int64_t n_write, const int32_t* prefix_groups,
+                                   int64_t n_groups, int64_t n_members, int64_t n_pages,
+                                   int64_t n_items, void* workspace, int64_t workspace_bytes,
+                                   void* stream);
 
 /*
  * Workspace bytes rlt_paged_prefill needs (shape-only, no sync needed).  Zero

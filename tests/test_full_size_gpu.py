@@ -256,7 +256,8 @@ def test_aliased_prefix_decode_full_size_64bit_pages():
 
     ops.kv_append(key_cache, value_cache, 0, blocks.to(dev), offsets.to(dev), k_new, v_new)
     tables_dev, lengths_dev = tables.to(dev), torch.tensor(lengths, dtype=torch.int32, device=dev)
-    hint = ops.shared_prefix(range(rows), prefix.tolist(), rows, lengths, dev)
+    hint = ops.prefix_groups([prefix.tolist()] * rows, lengths, PAGE, 1, dev)
+    assert hint.n_groups >= 1 and hint.n_members == rows
     out = ops.paged_decode(q, key_cache[:, 0], value_cache[:, 0], tables_dev, lengths_dev, shared_prefix=hint)
     plain = ops.paged_decode(q, key_cache[:, 0], value_cache[:, 0], tables_dev, lengths_dev)
     torch.cuda.synchronize()

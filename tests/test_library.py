@@ -75,16 +75,22 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     dst = native.int64_array([3])
     rc = lib.rlt_kv_copy_token(1, 1, strides, 3, dst, 1, 0, 1, 8, 4, 1, 8, 2, None)
     assert rc == native.RLT_EINVAL and "source" in native.last_error()
-    # Shared-prefix hint: missing arrays, member count, split length and prefix width.
-    decode = (1, strides, 1, 1, strides, 1, 64, 64, 1, 1, strides, 4, 16, 16, 128, 16, 4096, 1.0, 2, 16, 1 << 30)
-    rc = lib.rlt_paged_decode_shared_prefix(*decode, None, 1, 2, 1, 32, 512, None)
-    assert rc == native.RLT_EINVAL and "NULL prefix" in native.last_error()
-    rc = lib.rlt_paged_decode_shared_prefix(*decode, 1, 1, 5, 1, 32, 512, None)
-    assert rc == native.RLT_EINVAL and "n_prefix_rows" in native.last_error()
-    rc = lib.rlt_paged_decode_shared_prefix(*decode, 1, 1, 2, 1, 32, 384, None)
-    assert rc == native.RLT_EINVAL and "prefix_split_len" in native.last_error()
-    rc = lib.rlt_paged_decode_shared_prefix(*decode, 1, 1, 2, 1, 65, 512, None)
-    assert rc == native.RLT_EINVAL and "prefix_pages" in native.last_error()
+    # Prefix groups: missing buffer, group, member and page counts.
+    decode = (1, strides, 1, 1, strides, 1, 64, 64, 1, 1, strides, 4, 16, 16, 128, 16, 4096, 1.0, 2)
+    append = (None, None, None, None, None, None, 0)
+    tail = (16, 1 << 30, None)
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, None, 1, 2, 32, 32, *tail)
+    assert rc == native.RLT_EINVAL and "NULL prefix_groups" in native.last_error()
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 0, 2, 32, 32, *tail)
+    assert rc == native.RLT_EINVAL and "n_groups" in native.last_error()
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 1, 5, 32, 32, *tail)
+    assert rc == native.RLT_EINVAL and "n_members" in native.last_error()
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 1, 2, 0, 32, *tail)
+    assert rc == native.RLT_EINVAL and "n_pages" in native.last_error()
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 1, 2, 65, 32, *tail)
+    assert rc == native.RLT_EINVAL and "n_pages" in native.last_error()
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 1, 2, 32, -1, *tail)
+    assert rc == native.RLT_EINVAL and "n_items" in native.last_error()
 
 
 def test_workspace_sizes_depend_only_on_shape():

@@ -112,14 +112,20 @@ struct DecodeArgs {
   int64_t num_blocks;
   int64_t max_len;  // table width * page: lengths are clamped to what the table covers
   float qscale;     // softmax scale * log2(e)
-  // Shared prefix (all null / 0 when absent): rows with prefix_member[r] != 0
-  // begin with the prefix_pages pages of prefix_table; prefix_rows lists
-  // exactly those rows.  Their splits inside the prefix (at split length
-  // prefix_split_len) come from shared_prefix_kernel instead of the split pass.
-  const int32_t* prefix_member;
-  const int32_t* prefix_rows;
-  const int32_t* prefix_table;
-  int n_prefix_rows, prefix_pages, prefix_split_len;
+  // Prefix groups (all null / 0 when absent; the layout of the hint buffer is
+  // documented at rlt_paged_decode_shared_prefix in rlt_kv.h): row r belongs
+  // to group pg_row_group[r] (-1: none); group g's record is (first member,
+  // member count, first page, page count, split length) at pg_groups[5g];
+  // its member rows and shared page ids are slices of pg_members / pg_pages;
+  // pg_item_start[g] is the first prefix-pass work item of group g.  The
+  // splits of a member row inside its group's pages (at the group's split
+  // length) come from shared_prefix_kernel instead of the split pass.
+  const int32_t* pg_row_group;
+  const int32_t* pg_groups;
+  const int32_t* pg_item_start;
+  const int32_t* pg_members;
+  const int32_t* pg_pages;
+  int pg_n_groups, pg_n_members, pg_n_pages, pg_n_items;
   // Fused KV append (rlt_paged_decode_append; null / 0 otherwise): row
   // r < n_write stores its new token k_new[r] / v_new[r] ([hkv, D], strides
   // in elements, dim stride 1) at slot (write_blocks[r], write_offsets[r]) of
@@ -141,19 +147,39 @@ __device__ __forceinline__ int row_length(const DecodeArgs& a, int r) {
   return static_cast<int>(len < a.max_len ? len : a.max_len);
 }
 
+// Group record fields (pg_groups[5g + field]).
+constexpr int kGroupMember0 = 0, kGroupMembers = 1, kGroupPage0 = 2, kGroupPages = 3, kGroupSplit = 4;
+constexpr int kGroupFields = 5;
+
+// The record of group g when its member and page slices lie inside the hint
+// buffers and its split length is one the decode plan uses; null otherwise
+// (the group is then ignored).
+__device__ __forceinline__ const int32_t* group_record(const DecodeArgs& a, int g) {
+  if (g < 0 || g >= a.pg_n_groups) return nullptr;
+  const int32_t* rec = a.pg_groups + kGroupFields * g;
+  const int m0 = rec[kGroupMember0], mn = rec[kGroupMembers], p0 = rec[kGroupPage0], pn = rec[kGroupPages];
+  const int split = rec[kGroupSplit];
+  const bool ok = m0 >= 0 && mn >= 0 && m0 <= a.pg_n_members - mn && p0 >= 0 && pn >= 0 && p0 <= a.pg_n_pages - pn &&
+                  split >= kSplitTokens && (split & (split - 1)) == 0;
+  return ok ? rec : nullptr;
+}
+
 // True when split sp of row r (split_len tokens, ns splits) is computed by
 // shared_prefix_kernel rather than by the split pass.  Both kernels evaluate
-// this same predicate, so every split is produced exactly once.  The split
-// must lie inside the shared prefix, leave at least one split of the row to
-// the split pass (so the row goes through the merge), use the prefix pass's
-// split length, and read exactly the shared pages.
+// this same predicate, so every split is produced exactly once.  The row must
+// be in a group that uses its split length; the split must lie inside the
+// group's pages and leave at least one split of the row to the split pass (so
+// the row goes through the merge), and the row's table must hold exactly the
+// group's pages there.  All of it depends on the row and its own group only.
 __device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
-  if (!a.prefix_member || !a.prefix_member[r] || split_len != a.prefix_split_len) return false;
-  const int64_t covered = static_cast<int64_t>(a.prefix_pages) * a.page / split_len;
+  if (!a.pg_row_group) return false;
+  const int32_t* rec = group_record(a, a.pg_row_group[r]);
+  if (!rec || rec[kGroupSplit] != split_len) return false;
+  const int64_t covered = static_cast<int64_t>(rec[kGroupPages]) * a.page / split_len;
   if (sp >= covered || sp >= ns - 1) return false;
   const int pages = split_len / a.page;
   const int32_t* trow = a.tables + static_cast<int64_t>(r) * a.table_stride + sp * pages;
-  const int32_t* shared = a.prefix_table + sp * pages;
+  const int32_t* shared = a.pg_pages + rec[kGroupPage0] + sp * pages;
   bool same = true;
   for (int i = 0; i < pages; ++i) same &= trow[i] == shared[i];
   return same;
@@ -655,20 +681,26 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 }
 
 // Shared-prefix pass: the split partials of the splits that prefix_takes()
-// gives it, for every listed row at once.  Workgroup (sp, h, b) owns split sp
-// of the shared prefix (keys [sp * S, (sp + 1) * S) of prefix_table, S =
-// prefix_split_len) under kv head h, for 64 queries: (row, q head) pairs
-// b * 64 .. b * 64 + 63 of prefix_rows x G.  Wave w takes queries 32(w % 2) ..
-// + 31 over key half w / 2 of the split; the two halves merge their (max, sum,
-// acc) through LDS at the end.  K and V of each 32-key tile are read once into
-// LDS (row-major, padded rows) and serve all 64 queries, so the prefix is read
-// from memory once per launch instead of once per row.  Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32
-// K rows, B = its 32 queries' q), keeps an online softmax in log2 units (the
-// running maximum moves only when a tile exceeds it by 2^kRescale), and
+// gives it, for every group at once.  Work item i (blockIdx.x) belongs to the
+// group g with item_start[g] <= i < item_start[g + 1]; its offset in the group
+// is (split sp, block b of 64 queries), b fastest.  Workgroup (i, h) owns
+// split sp of group g's pages (keys [sp * S, (sp + 1) * S), S the group's
+// split length) under kv head h, for 64 queries: (row, q head) pairs
+// b * 64 .. b * 64 + 63 of the group's members x G.  Wave w takes queries
+// 32(w % 2) .. + 31 over key half w / 2 of the split; the two halves merge
+// their (max, sum, acc) through LDS at the end.  K and V of each 32-key tile
+// are read once into LDS (row-major, padded rows) and serve all 64 queries,
+// so a prefix is read from memory once per launch instead of once per row.
+// Per tile a wave forms S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32 K rows,
+// B = its 32 queries' q), keeps an online softmax in log2 units, and
 // accumulates O^T += V^T P^T with P rounded to T and V^T from transposing LDS
 // reads; the row sums come from the same rounded P through one MFMA against
-// ones.  The result is written as the split pass would: (max, sum) and the
-// unnormalised accumulator in the decode workspace slot of (row, h, sp).
+// ones.  A query's running maximum moves only when a tile exceeds it by
+// 2^kRescale, decided per query: with every MFMA column computed on its own,
+// a query's result depends on its own q and keys only, not on which queries
+// share the workgroup (so not on the batch).  The result is written as the
+// split pass would: (max, sum) and the unnormalised accumulator in the decode
+// workspace slot of (row, h, sp).
 constexpr int kPrefixBK = 32;   // keys per tile
 constexpr float kPrefixRescale = 8.f;
 
@@ -683,9 +715,28 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
   static_assert(2 * 64 * MERGE_FLOATS * 4 <= 2 * (KTILE + VTILE) * 2, "merge fits in the tile buffers");
   __shared__ __align__(16) uint16_t tiles[2 * (KTILE + VTILE)];  // per key half: K tile, V tile
 
-  const int sp = blockIdx.x;
+  const int item = blockIdx.x;
   const int h = blockIdx.y;
   const int tid = threadIdx.x;
+  // The item's group: the last g with item_start[g] <= item.
+  int g = 0;
+  {
+    int hi = a.pg_n_groups;
+    while (hi - g > 1) {
+      const int mid = (g + hi) >> 1;
+      if (a.pg_item_start[mid] <= item) g = mid;
+      else hi = mid;
+    }
+  }
+  const int32_t* rec = group_record(a, g);
+  if (!rec) return;
+  const int S = rec[kGroupSplit];
+  const int n_members = rec[kGroupMembers];
+  const int qblocks = (n_members * G + 63) / 64;
+  const int local = item - a.pg_item_start[g];
+  if (local < 0 || qblocks == 0) return;
+  const int sp = local / qblocks;
+  const int qblock = local - sp * qblocks;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
   const int qw = wave & 1;   // query half
@@ -695,13 +746,13 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
   uint16_t* const k_lds = tiles + kh * (KTILE + VTILE);
   uint16_t* const v_lds = k_lds + KTILE;
 
-  // This lane's query: (prefix_rows[qi / G], q head h * G + qi % G).
-  const int qi = blockIdx.z * 64 + qw * 32 + col;
-  const bool listed = qi < a.n_prefix_rows * G;
-  const int r = a.prefix_rows[listed ? qi / G : 0];
+  // This lane's query: (member qi / G of group g, q head h * G + qi % G).
+  const int qi = qblock * 64 + qw * 32 + col;
+  const bool listed = qi < n_members * G;
+  const int r = a.pg_members[rec[kGroupMember0] + (listed ? qi / G : 0)];
   const int j = listed ? qi % G : 0;
   bool mine = false;
-  if (listed && r >= 0 && r < a.n_rows) {
+  if (listed && r >= 0 && r < a.n_rows && a.pg_row_group[r] == g) {
     int split_len, ns;
     split_plan(row_length(a, r), &split_len, &ns);
     mine = prefix_takes(a, r, sp, split_len, ns);
@@ -719,7 +770,7 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
 
   // Staging: within a key half, thread t (of 128) moves 16-byte chunk
   // (t + 128i) % 16 of tile row (t + 128i) / 16, i = 0..3, for K and for V.
-  const int S = a.prefix_split_len;
+  const int32_t* group_pages = a.pg_pages + rec[kGroupPage0];
   const int ntiles = S / kPrefixBK / 2;  // per key half
   const int key0 = sp * S + kh * ntiles * kPrefixBK;
   const int ltid = tid & 127;
@@ -732,7 +783,7 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int c = ltid + 128 * i;
       const int key = key0 + t * kPrefixBK + (c >> 4);
-      const int64_t b = a.prefix_table[key / a.page];
+      const int64_t b = group_pages[key / a.page];
       const int64_t blk = (b < 0 || b >= a.num_blocks) ? 0 : b;
       const int64_t off = blk * a.kv_block + static_cast<int64_t>(key % a.page) * a.kv_token + (c & 15) * 8;
       kr[i] = load_page(reinterpret_cast<const u32x4*>(kbase + off));
@@ -776,9 +827,12 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
       tmax = fmaxf(tmax, sacc[e]);
     }
     tmax = max_across_halves(tmax);
-    if (__builtin_amdgcn_ballot_w64(tmax > m + kPrefixRescale) != 0) {
-      const float mn = fmaxf(m, tmax);
-      const float corr = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+    // Both lanes of a query (col, col + 32) hold the same tmax and m, so they
+    // decide alike; a query that does not move keeps corr = 1 (exact).
+    const bool move = tmax > m + kPrefixRescale;
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float mn = move ? fmaxf(m, tmax) : m;
+      const float corr = (!move || mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
 #pragma unroll
       for (int c = 0; c < DTILES; ++c)
 #pragma unroll
@@ -936,14 +990,11 @@ DecodeKernel pick_group(int G) {
   }
 }
 
-// The fused-append split pass is compiled for the XCD-affine schedule without
-// the shared-prefix check; other cases append first, then decode.
+// The fused-append split pass is compiled for the XCD-affine schedule (with
+// and without the shared-prefix check); other cases append first, then decode.
 template <typename T, int D, bool PREFIX>
 DecodeKernel pick_group(int G, bool xcd, bool append) {
-  if (append) {
-    if constexpr (!PREFIX) return xcd ? pick_group<T, D, true, false, true>(G) : nullptr;
-    return nullptr;
-  }
+  if (append) return xcd ? pick_group<T, D, true, PREFIX, true>(G) : nullptr;
   return xcd ? pick_group<T, D, true, PREFIX, false>(G) : pick_group<T, D, false, PREFIX, false>(G);
 }
 
@@ -1007,31 +1058,21 @@ __global__ __launch_bounds__(64) void slice_append_kernel(DecodeArgs a) {
 
 bool stride16(int64_t stride, int esize) { return (stride * esize) % 16 == 0; }
 
-// Launches the shared-prefix pass; false when it does not exist for this
-// shape (the caller then drops the hint and the split pass computes every
-// split itself).
+// The shared-prefix pass for this shape, or null where it does not exist
+// (the caller then drops the hint and the split pass computes every split).
 template <typename T>
-bool launch_shared_prefix(const DecodeArgs& a, hipStream_t stream) {
+DecodeKernel shared_prefix_pass(int d, int G) {
   if constexpr (std::is_same_v<T, float>) {
-    return false;
+    return nullptr;
   } else {
-    if (a.d != 128) return false;
-    void (*kernel)(DecodeArgs) = nullptr;
-    switch (a.hq / a.hkv) {
-      case 1: kernel = shared_prefix_kernel<T, 1>; break;
-      case 2: kernel = shared_prefix_kernel<T, 2>; break;
-      case 4: kernel = shared_prefix_kernel<T, 4>; break;
-      case 8: kernel = shared_prefix_kernel<T, 8>; break;
-      default: return false;
+    if (d != 128) return nullptr;
+    switch (G) {
+      case 1: return shared_prefix_kernel<T, 1>;
+      case 2: return shared_prefix_kernel<T, 2>;
+      case 4: return shared_prefix_kernel<T, 4>;
+      case 8: return shared_prefix_kernel<T, 8>;
+      default: return nullptr;
     }
-    const int64_t splits = std::min<int64_t>(static_cast<int64_t>(a.prefix_pages) * a.page / a.prefix_split_len,
-                                             kMaxSplits - 1);
-    if (splits <= 0) return false;
-    const int64_t queries = static_cast<int64_t>(a.n_prefix_rows) * (a.hq / a.hkv);
-    const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a.hkv),
-                    static_cast<unsigned>((queries + 63) / 64));
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a);
-    return true;
   }
 }
 
@@ -1046,13 +1087,20 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
                          stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
                          a.kv_token * a.page < (int64_t(1) << 31);
   const bool xcd = RLT_DECODE_XCD_SCHEDULE && a.hkv % kWaves == 0;
+  // The prefix groups are served where the prefix pass and a split pass with
+  // the prefix check exist for this shape; elsewhere the hint is dropped.
+  const DecodeKernel prefix_pass =
+      (a.pg_row_group && a.pg_n_items > 0 && layout_ok && pick_tiled<T>(a.d, G, xcd, true, false))
+          ? shared_prefix_pass<T>(a.d, G)
+          : nullptr;
+  if (!prefix_pass) a.pg_row_group = nullptr;
+  const bool prefix = prefix_pass != nullptr;
   if (a.n_write > 0) {
     // The fused append needs the tiled kernel and 16-byte rows of k_new / v_new;
     // otherwise the new tokens are written first and the decode runs as usual.
-    const bool fused = layout_ok && !a.prefix_member && a.kn_dim == 1 && a.vn_dim == 1 && aligned16(a.k_new) &&
-                       aligned16(a.v_new) &&
+    const bool fused = layout_ok && a.kn_dim == 1 && a.vn_dim == 1 && aligned16(a.k_new) && aligned16(a.v_new) &&
                        stride16(a.kn_row, esize) && stride16(a.kn_head, esize) && stride16(a.vn_row, esize) &&
-                       stride16(a.vn_head, esize) && pick_tiled<T>(a.d, G, xcd, false, true) != nullptr;
+                       stride16(a.vn_head, esize) && pick_tiled<T>(a.d, G, xcd, prefix, true) != nullptr;
     if (!fused) {
       hipLaunchKernelGGL(slice_append_kernel<T>, dim3(a.n_write, a.hkv), dim3(64), 0, stream, a);
       if (int rc = check_launch("rlt_paged_decode_append(append)")) return rc;
@@ -1060,11 +1108,13 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
     }
   }
   const bool append = a.n_write > 0;
-  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, false, append);
-  if (a.prefix_member && !(tiled && launch_shared_prefix<T>(a, stream))) a.prefix_member = nullptr;
-  if (a.prefix_member) {
+  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, prefix, append);
+  if (prefix) {
+    // The prefix splits are never a row's last split, which holds the new
+    // token, so the prefix pass reads no slot the fused append writes.
+    hipLaunchKernelGGL(prefix_pass, dim3(static_cast<unsigned>(a.pg_n_items), static_cast<unsigned>(a.hkv)),
+                       dim3(256), 0, stream, a);
     if (int rc = check_launch("rlt_paged_decode_shared_prefix(prefix)")) return rc;
-    tiled = pick_tiled<T>(a.d, G, xcd, true, append);
   }
   if (!tiled) {
     if (a.d > 64 * kGenericMaxPerLane) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: head_dim > 512");
@@ -1135,12 +1185,10 @@ extern "C" int64_t rlt_paged_decode_workspace_bytes(int64_t n_rows, int64_t num_
 
 namespace {
 
+// Sections of the prefix-group hint buffer (rlt_kv.h).
 struct PrefixHint {
-  const int32_t* member;
-  const int32_t* rows;
-  int64_t n_rows;
-  const int32_t* table;
-  int64_t pages, split_len;
+  const int32_t* buffer;
+  int64_t n_groups, n_members, n_pages, n_items;
 };
 
 struct AppendSource {
@@ -1205,12 +1253,15 @@ int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
   a.max_len = max_table_width * page_size;
   a.qscale = scale * kLog2e;
   if (hint) {
-    a.prefix_member = hint->member;
-    a.prefix_rows = hint->rows;
-    a.n_prefix_rows = static_cast<int>(hint->n_rows);
-    a.prefix_table = hint->table;
-    a.prefix_pages = static_cast<int>(hint->pages);
-    a.prefix_split_len = static_cast<int>(hint->split_len);
+    a.pg_row_group = hint->buffer;
+    a.pg_groups = a.pg_row_group + n_rows;
+    a.pg_item_start = a.pg_groups + kGroupFields * hint->n_groups;
+    a.pg_members = a.pg_item_start + hint->n_groups + 1;
+    a.pg_pages = a.pg_members + hint->n_members;
+    a.pg_n_groups = static_cast<int>(hint->n_groups);
+    a.pg_n_members = static_cast<int>(hint->n_members);
+    a.pg_n_pages = static_cast<int>(hint->n_pages);
+    a.pg_n_items = static_cast<int>(hint->n_items);
   }
   if (append) {
     if (append->n_write < 0 || append->n_write > n_rows)
@@ -1373,27 +1424,27 @@ extern "C" int rlt_paged_decode_append(
 }
 
 extern "C" int rlt_paged_decode_shared_prefix(
-    const void* q, const int64_t* q_strides, const void* key_cache, const void* value_cache,
-    const int64_t* kv_strides, const int32_t* block_tables, int64_t table_stride, int64_t max_table_width,
-    const int32_t* context_lengths, void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads,
-    int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_blocks, float scale, int dtype,
-    void* workspace, int64_t workspace_bytes, const int32_t* prefix_member, const int32_t* prefix_rows,
-    int64_t n_prefix_rows, const int32_t* prefix_table, int64_t prefix_pages, int64_t prefix_split_len,
-    void* stream) {
-  if (!prefix_member || !prefix_rows || !prefix_table)
-    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: NULL prefix argument");
-  if (n_prefix_rows < 1 || n_prefix_rows > n_rows)
-    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_prefix_rows must be in [1, n_rows]");
+    const void* q, const int64_t* q_strides, void* key_cache, void* value_cache, const int64_t* kv_strides,
+    const int32_t* block_tables, int64_t table_stride, int64_t max_table_width, const int32_t* context_lengths,
+    void* out, const int64_t* out_strides, int64_t n_rows, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t page_size, int64_t num_blocks, float scale, int dtype, const void* k_new,
+    const int64_t* k_new_strides, const void* v_new, const int64_t* v_new_strides, const int64_t* write_blocks,
+    const int64_t* write_offsets, int64_t n_write, const int32_t* prefix_groups, int64_t n_groups,
+    int64_t n_members, int64_t n_pages, int64_t n_items, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!prefix_groups) return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: NULL prefix_groups");
   if (n_rows > kMaxRowsPerLaunch)
     return fail(RLT_EUNSUPPORTED, "rlt_paged_decode_shared_prefix: more than %d rows", kMaxRowsPerLaunch);
-  if (prefix_split_len < kSplitTokens || (prefix_split_len & (prefix_split_len - 1)) || page_size <= 0 ||
-      prefix_split_len % page_size)
-    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: prefix_split_len must be %d << k and a page multiple",
-                kSplitTokens);
-  if (prefix_pages < 1 || prefix_pages > max_table_width)
-    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: prefix_pages must be in [1, max_table_width]");
-  const PrefixHint hint{prefix_member, prefix_rows, n_prefix_rows, prefix_table, prefix_pages, prefix_split_len};
+  if (n_groups < 1 || n_groups > n_rows)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_groups must be in [1, n_rows]");
+  if (n_members < n_groups || n_members > n_rows)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_members must be in [n_groups, n_rows]");
+  if (n_pages < 1 || n_pages > n_groups * max_table_width)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_pages must be in [1, n_groups x max_table_width]");
+  if (n_items < 0 || n_items > 0x7fffffff)
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_items out of range");
+  const PrefixHint hint{prefix_groups, n_groups, n_members, n_pages, n_items};
+  const AppendSource append{k_new, k_new_strides, v_new, v_new_strides, write_blocks, write_offsets, n_write};
   return paged_decode(q, q_strides, key_cache, value_cache, kv_strides, block_tables, table_stride, max_table_width,
                       context_lengths, out, out_strides, n_rows, num_q_heads, num_kv_heads, head_dim, page_size,
-                      num_blocks, scale, dtype, workspace, workspace_bytes, stream, &hint);
+                      num_blocks, scale, dtype, workspace, workspace_bytes, stream, &hint, &append);
 }

@@ -89,8 +89,9 @@ SIGNATURES = {
         c_int,
         [c_void_p, _i64p, c_void_p, c_void_p, _i64p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, _i64p]
         + [c_int64] * 6
-        + [c_float, c_int, c_void_p, c_int64]
-        + [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p],
+        + [c_float, c_int, c_void_p, _i64p, c_void_p, _i64p, c_void_p, c_void_p, c_int64]
+        + [c_void_p] + [c_int64] * 4
+        + [c_void_p, c_int64, c_void_p],
     ),
     "rlt_paged_prefill_workspace_bytes": (c_int64, [c_int64] * 7 + [c_int]),
     "rlt_paged_prefill": (

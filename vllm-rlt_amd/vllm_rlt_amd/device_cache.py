@@ -45,5 +45,5 @@ class DeviceCache:
         cache = self.cache
         return cache.attention.decode_append(
             q, cache.key_cache[:, layer], cache.value_cache[:, layer], batch.block_tables, batch.context_lengths,
-            k, v, batch.write_blocks, batch.write_offsets,
+            k, v, batch.write_blocks, batch.write_offsets, shared_prefix=getattr(batch, "shared_prefix", None),
         )

@@ -51,7 +51,7 @@ class KVCacheManager(KVPageBook):
         enable_prefix_caching: bool = False,
         incremental_allocation: bool = False,
         watermark_ratio: float = 0.0,
-        share_prefix_reads: bool = False,
+        share_prefix_reads: bool = True,
     ):
         super().__init__(
             num_layers,
@@ -74,11 +74,13 @@ class KVCacheManager(KVPageBook):
             raise ValueError("the hip attention backend requires a ROCm device")
         self.backend = backend
         self.dtype = dtype
-        # Decode batches whose rows alias prefix pages read them once per
-        # launch (rlt_paged_decode_shared_prefix).  Off by default: a row's
-        # output bits then depend on which rows share its batch (within the
-        # attention tolerance), where otherwise they depend on the row alone.
+        # Decode rows whose pages came from the prefix cache read those pages
+        # once per launch for all rows that share them, one group per plane
+        # and prefix (rlt_paged_decode_shared_prefix).  Which splits take that
+        # path depends on the row's own allocation, and each row's result on
+        # its own q and pages, so a row's bits do not depend on the batch.
         self.share_prefix_reads = bool(share_prefix_reads)
+        self._query_group = 8  # q heads per KV head, learnt from the first attention call
         self.attention = HipPagedAttention(device, dtype, self.head_dim, self.block_size)
         self.attention_info = self.attention.info
         shape = (self.num_blocks, self.num_layers, self.block_size, self.num_kv_heads, self.head_dim)
@@ -101,9 +103,16 @@ class KVCacheManager(KVPageBook):
         t, w = plan.tables.shape
         s = 0 if plan.cu_seqlens is None else len(plan.cu_seqlens)
         found = None
-        if self.share_prefix_reads and plan.cu_seqlens is None:
-            found = ops.find_shared_prefix(plan.tables, plan.lengths, self.block_size)
-        hint32 = 0 if found is None else t + len(found[0]) + len(found[1])
+        if self.share_prefix_reads and plan.cu_seqlens is None and len(plan.rows) == t:
+            row_pages = [
+                allocation.block_tables[self._plane(depth)][: allocation.prefix_pages] if allocation.prefix_pages else ()
+                for allocation, depth, _ in plan.rows
+            ]
+            # The prefix pass's item counts depend on the q heads per KV head,
+            # which the first attention call tells; until then they are sized
+            # for the widest group it serves.
+            found = ops.prefix_group_layout(row_pages, plan.lengths, self.block_size, self._query_group)
+        hint32 = 0 if found is None else len(found[0])
         n64 = 3 * n
         n32 = t * w + t + s + hint32
         bytes64 = 8 * n64
@@ -122,11 +131,7 @@ class KVCacheManager(KVPageBook):
                 h32[t * w + t : t * w + t + s] = plan.cu_seqlens
             if found is not None:
                 base = t * w + t + s
-                member = h32[base : base + t]
-                member[:] = 0
-                member[found[0]] = 1
-                h32[base + t : base + t + len(found[0])] = found[0]
-                h32[base + t + len(found[0]) : base + hint32] = found[1]
+                h32[base : base + hint32] = found[0]
         dev = host.to(self.device, non_blocking=True)
         d64 = dev[:bytes64].view(torch.int64) if n64 else torch.empty(0, dtype=torch.int64, device=self.device)
         d32 = (
@@ -146,19 +151,13 @@ class KVCacheManager(KVPageBook):
             writable=plan.writable,
             cu_seqlens_q=d32[t * w + t : t * w + t + s] if s else None,
             max_seqlen_q=plan.max_seqlen_q,
-            shared_prefix=None if found is None else self._shared_prefix_views(d32, t * w + t + s, t, found),
+            shared_prefix=None if found is None else self._prefix_groups_view(d32, t * w + t + s, t, found),
         )
 
     @staticmethod
-    def _shared_prefix_views(d32, base, t, found):
-        rows, pages, split_len = found
-        m = len(rows)
-        return ops.SharedPrefix(
-            member=d32[base : base + t],
-            rows=d32[base + t : base + t + m],
-            table=d32[base + t + m : base + t + m + len(pages)],
-            split_len=split_len,
-        )
+    def _prefix_groups_view(d32, base, t, found):
+        hint, *counts = found
+        return ops.PrefixGroups(d32[base : base + len(hint)], t, *counts)
 
     # ------------------------------------------------------------ tensors
     def _validate_tensor(self, tensor, batch_size, name, *, query=False) -> None:
@@ -168,6 +167,7 @@ class KVCacheManager(KVPageBook):
         if query:
             if tensor.shape[1] == 0 or tensor.shape[1] % self.num_kv_heads:
                 raise ValueError("query heads must be a positive multiple of KV heads")
+            self._query_group = min(tensor.shape[1] // self.num_kv_heads, 64)
         elif tensor.shape[1] != self.num_kv_heads:
             raise ValueError(f"{name} must have {self.num_kv_heads} KV heads")
         if tensor.device != self.device or tensor.dtype != self.dtype:
@@ -286,10 +286,11 @@ class KVCacheManager(KVPageBook):
         """_write_prepared then _attend_prepared (:520-586) as one launch where that gives the same bits.
 
         A decode batch whose rows are independent (_rows_independent) runs
-        rlt_paged_decode_append; any other batch (packed prefill, a request
-        twice on one plane, a shared-prefix hint) runs the two steps.
+        rlt_paged_decode_append (rlt_paged_decode_shared_prefix with its
+        append when the batch carries prefix groups); any other batch (packed
+        prefill, a request twice on one plane) runs the two steps.
         """
-        if not self._rows_independent(batch) or getattr(batch, "shared_prefix", None) is not None:
+        if not self._rows_independent(batch):
             self._write_prepared(layer, batch, k, v)
             return self._attend_prepared(layer, batch, q)
         self._validate_layer(layer)
@@ -308,6 +309,7 @@ class KVCacheManager(KVPageBook):
         out = self.attention.decode_append(
             q, self.key_cache[:, layer], self.value_cache[:, layer], batch.block_tables, batch.context_lengths,
             k, v, batch.write_blocks, batch.write_offsets, n_write=len(batch.rows),
+            shared_prefix=getattr(batch, "shared_prefix", None),
         )
         self._record_written(batch, layer)
         return out

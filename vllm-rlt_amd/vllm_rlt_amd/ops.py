@@ -284,77 +284,88 @@ def decode_split_len(length: int) -> int:
     return per
 
 
+GROUP_FIELDS = 5  # (first member, member count, first page, page count, split length)
+
+
 @dataclass(frozen=True)
-class SharedPrefix:
-    """Rows of a decode batch whose block tables begin with the same pages.
+class PrefixGroups:
+    """Decode rows grouped by the prefix-cache pages their tables begin with.
 
-    member: int32 [rows], 1 for those rows.  rows: int32 [n], the same rows.
-    table: int32 [pages], the shared page ids.  split_len: the decode split
-    length (decode_split_len) of the member rows the prefix pass serves.
+    `hint` is the int32 device buffer rlt_paged_decode_shared_prefix reads:
+    row_group [n_rows] (-1: none), n_groups records of (first member, member
+    count, first page, page count, split length), item_start [n_groups + 1],
+    the member rows of every group, then every group's shared page ids.
     """
 
-    member: torch.Tensor
-    rows: torch.Tensor
-    table: torch.Tensor
-    split_len: int
+    hint: torch.Tensor
+    n_rows: int
+    n_groups: int
+    n_members: int
+    n_pages: int
+    n_items: int
+    group_size: int  # q heads per KV head the item counts were sized for (at least the call's)
 
 
-def find_shared_prefix(tables, lengths, page: int):
-    """(rows, pages, split_len) of rows whose block tables begin with the same pages, or None.
+def prefix_group_layout(row_pages, lengths, page: int, group_size: int):
+    """Host int32 hint and its counts (n_groups, n_members, n_pages, n_items, group_size), or None.
 
-    tables: int32 [rows, W] host array (-1 padded); lengths: the rows' context
-    lengths.  Candidates are the live rows sharing the most common first page.
-    Each has a common prefix with the first of them (up to the first differing
-    or negative entry); of the prefix lengths that cover whole splits, the one
-    that saves the most split reads ((members - 1) x whole splits) wins, with
-    the rows whose common prefix reaches it.  None when that saves nothing.
+    row_pages[r]: the prefix-cache page ids row r's table begins with (empty
+    or None: the row reads no shared prefix).  Rows group by those pages cut
+    to whole splits of their own split length (decode_split_len of their
+    length), and by that split length; rows whose pages cover no whole split
+    stay out.  group_size is the number of q heads per KV head (a larger value
+    only adds empty work items; the hint serves calls up to it).  Groups appear
+    in first-member order and list members in batch order, so the layout is a
+    function of the rows alone.
     """
-    tables = np.asarray(tables)
-    lengths = np.asarray(lengths)
-    if tables.ndim != 2 or len(tables) < 2 or tables.shape[1] == 0:
+    n_rows = len(row_pages)
+    if len(lengths) != n_rows:
+        raise ValueError("one length per row")
+    groups: dict = {}
+    row_group = np.full(n_rows, -1, dtype=np.int32)
+    for r, (pages, n) in enumerate(zip(row_pages, lengths)):
+        if pages is None or not len(pages) or int(n) <= 0:
+            continue
+        split = decode_split_len(int(n))
+        covered = len(pages) * page // split
+        if covered == 0:
+            continue
+        key = (tuple(int(b) for b in pages[: covered * split // page]), split)
+        row_group[r] = groups.setdefault(key, len(groups))
+    if not groups:
         return None
-    first = tables[:, 0]
-    valid = (first >= 0) & (lengths > 0)
-    values, counts = np.unique(first[valid], return_counts=True)
-    if not len(counts) or counts.max() < 2:
-        return None
-    rows = np.nonzero(valid & (first == values[counts.argmax()]))[0]
-    group = tables[rows]
-    eq = (group == group[0]) & (group[0] >= 0)
-    common = np.where(eq.all(axis=1), eq.shape[1], np.argmin(eq, axis=1))
-    splits = [decode_split_len(n) for n in lengths[rows]]
-    split_len = max(set(splits), key=splits.count)
-    best, best_gain = None, 0
-    for shared in sorted(set(common.tolist())):
-        members = int((common >= shared).sum())
-        gain = (members - 1) * (shared * page // split_len)
-        if gain > best_gain:
-            best, best_gain = shared, gain
-    if best is None:
-        return None
-    return rows[common >= best].tolist(), group[0, :best].tolist(), split_len
+    members = [[] for _ in groups]
+    for r in np.nonzero(row_group >= 0)[0]:
+        members[row_group[r]].append(int(r))
+    records, item_start, pages_flat = [], [0], []
+    member0 = 0
+    for (pages, split), g in groups.items():
+        count = len(members[g])
+        splits = min(len(pages) * page // split, DECODE_MAX_SPLITS - 1)
+        records.append((member0, count, len(pages_flat), len(pages), split))
+        item_start.append(item_start[-1] + splits * (-(-count * group_size // 64)))
+        pages_flat.extend(pages)
+        member0 += count
+    flat_members = [r for m in members for r in m]
+    hint = np.concatenate(
+        [
+            row_group,
+            np.asarray(records, dtype=np.int32).reshape(-1),
+            np.asarray(item_start, dtype=np.int32),
+            np.asarray(flat_members, dtype=np.int32),
+            np.asarray(pages_flat, dtype=np.int32),
+        ]
+    ).astype(np.int32)
+    return hint, len(groups), len(flat_members), len(pages_flat), item_start[-1], int(group_size)
 
 
-def shared_prefix(rows, pages, n_rows: int, lengths, device) -> SharedPrefix:
-    """A SharedPrefix for `rows` (indices into the batch) sharing page ids `pages`.
-
-    `lengths` are the member rows' context lengths (host values) and pick the
-    split length most of them use; members with another split length read the
-    prefix in the split pass, as without the hint.
-    """
-    rows = [int(r) for r in rows]
-    if not rows or len(set(rows)) != len(rows) or min(rows) < 0 or max(rows) >= n_rows:
-        raise ValueError("shared-prefix rows must be distinct batch rows")
-    splits = [decode_split_len(n) for n in lengths]
-    split_len = max(set(splits), key=splits.count) if splits else DECODE_SPLIT_TOKENS
-    member = torch.zeros(n_rows, dtype=torch.int32)
-    member[rows] = 1
-    return SharedPrefix(
-        member=member.to(device),
-        rows=torch.tensor(rows, dtype=torch.int32).to(device),
-        table=torch.as_tensor(pages, dtype=torch.int32).to(device),
-        split_len=split_len,
-    )
+def prefix_groups(row_pages, lengths, page: int, group_size: int, device) -> PrefixGroups | None:
+    """The PrefixGroups of a decode batch on `device` (prefix_group_layout), or None."""
+    layout = prefix_group_layout(row_pages, lengths, page, group_size)
+    if layout is None:
+        return None
+    hint, *counts = layout
+    return PrefixGroups(torch.from_numpy(hint).to(device), len(row_pages), *counts)
 
 
 def _decode_inputs(q, key_cache, value_cache, block_tables, context_lengths, out):
@@ -393,6 +404,27 @@ def _decode_workspace(workspace, rows, hq, hkv, d, device):
     return workspace
 
 
+def _serves(groups: PrefixGroups | None, rows: int, group_size: int) -> bool:
+    """Whether a hint applies: batches above the row limit, or with more q heads per
+    KV head than its items were sized for, read their prefixes per row (the hint
+    is an optimisation only)."""
+    return groups is not None and rows <= DECODE_SHARED_PREFIX_MAX_ROWS and group_size <= groups.group_size
+
+
+def _prefix_call(groups: PrefixGroups, rows: int, block_tables: torch.Tensor):
+    """Checked ctypes arguments of a PrefixGroups hint (rlt_paged_decode_shared_prefix)."""
+    if not 0 < groups.group_size <= 64:
+        raise ValueError("prefix groups need a group size in [1, 64]")
+    _require_rocm(groups.hint)
+    _require_int(groups.hint, torch.int32, "prefix groups")
+    size = rows + (GROUP_FIELDS + 1) * groups.n_groups + 1 + groups.n_members + groups.n_pages
+    if groups.n_rows != rows or groups.hint.numel() != size or not groups.hint.is_contiguous():
+        raise ValueError(f"prefix groups must be a contiguous int32 hint for {rows} rows")
+    if groups.n_pages > groups.n_groups * block_tables.shape[1]:
+        raise ValueError("a prefix group is wider than the block tables")
+    return [groups.hint.data_ptr(), groups.n_groups, groups.n_members, groups.n_pages, groups.n_items]
+
+
 def paged_decode_append(
     q: torch.Tensor,
     key_cache: torch.Tensor,
@@ -407,13 +439,16 @@ def paged_decode_append(
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     scale: float | None = None,
+    shared_prefix: PrefixGroups | None = None,
 ) -> torch.Tensor:
     """KV append of rows [0, n_write) then decode attention, in one launch (rlt_paged_decode_append).
 
     key_cache / value_cache are layer slices [blocks, page, kv_heads, head_dim]
     and are written.  Same pages and output bits as kv_append followed by
     paged_decode, provided no row reads a slot another row writes (a decode
-    batch with one row per request and depth).
+    batch with one row per request and depth).  With `shared_prefix` the
+    groups' prefix pages are read once per launch
+    (rlt_paged_decode_shared_prefix with its append arguments).
     """
     device, rows, hq, hkv, d, page, nb, out = _decode_inputs(q, key_cache, value_cache, block_tables, context_lengths, out)
     _require_rocm(q, k_new, v_new, write_blocks, write_offsets)
@@ -429,14 +464,21 @@ def paged_decode_append(
         return out
     workspace = _decode_workspace(workspace, rows, hq, hkv, d, device)
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    rc = _native.load().rlt_paged_decode_append(
+    common = [
         q.data_ptr(), int64_array(q.stride()), key_cache.data_ptr(), value_cache.data_ptr(),
         int64_array(key_cache.stride()), block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
         context_lengths.data_ptr(), out.data_ptr(), int64_array(out.stride()), rows, hq, hkv, d, page, nb, scale,
         dtype_code(q.dtype), k_new.data_ptr(), int64_array(k_new.stride()), v_new.data_ptr(),
-        int64_array(v_new.stride()), write_blocks.data_ptr(), write_offsets.data_ptr(), n, workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), stream_handle(device),
-    )
+        int64_array(v_new.stride()), write_blocks.data_ptr(), write_offsets.data_ptr(), n,
+    ]
+    tail = [workspace.data_ptr(), workspace.numel() * workspace.element_size(), stream_handle(device)]
+    if _serves(shared_prefix, rows, hq // hkv):
+        rc = _native.load().rlt_paged_decode_shared_prefix(
+            *common, *_prefix_call(shared_prefix, rows, block_tables), *tail
+        )
+        check(rc, "rlt_paged_decode_shared_prefix")
+        return out
+    rc = _native.load().rlt_paged_decode_append(*common, *tail)
     check(rc, "rlt_paged_decode_append")
     return out
 
@@ -450,13 +492,13 @@ def paged_decode(
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     scale: float | None = None,
-    shared_prefix: SharedPrefix | None = None,
+    shared_prefix: PrefixGroups | None = None,
 ) -> torch.Tensor:
     """Paged decode attention over layer-slice caches [blocks, page, kv_heads, head_dim].
 
     Same contract as torch_paged_attention (vllm_rlt/kernels/paged_attention.py:12-36):
-    returns a new tensor like q unless out is given.  With `shared_prefix` the
-    listed rows' common prefix pages are read once for all of them
+    returns a new tensor like q unless out is given.  With `shared_prefix` each
+    group's prefix pages are read once for all its rows
     (rlt_paged_decode_shared_prefix); the result is the same attention.
     """
     device, rows, hq, hkv, d, page, nb, out = _decode_inputs(q, key_cache, value_cache, block_tables, context_lengths, out)
@@ -464,27 +506,14 @@ def paged_decode(
         return out
     workspace = _decode_workspace(workspace, rows, hq, hkv, d, device)
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    if shared_prefix is not None and rows > DECODE_SHARED_PREFIX_MAX_ROWS:
-        shared_prefix = None  # an optimisation only: larger batches read the prefix per row
-    if shared_prefix is not None:
-        sp = shared_prefix
-        _require_rocm(sp.member, sp.rows, sp.table)
-        _require_int(sp.member, torch.int32, "shared_prefix.member")
-        _require_int(sp.rows, torch.int32, "shared_prefix.rows")
-        _require_int(sp.table, torch.int32, "shared_prefix.table")
-        if sp.member.shape != (rows,) or not sp.member.is_contiguous():
-            raise ValueError("shared_prefix.member must be contiguous int32 [rows]")
-        if not sp.rows.is_contiguous() or not sp.table.is_contiguous():
-            raise ValueError("shared_prefix rows and table must be contiguous")
-        if sp.table.numel() > block_tables.shape[1]:
-            raise ValueError("the shared prefix is wider than the block tables")
+    if _serves(shared_prefix, rows, hq // hkv):
         rc = _native.load().rlt_paged_decode_shared_prefix(
             q.data_ptr(), int64_array(q.stride()), key_cache.data_ptr(), value_cache.data_ptr(),
             int64_array(key_cache.stride()), block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
             context_lengths.data_ptr(), out.data_ptr(), int64_array(out.stride()), rows, hq, hkv, d, page, nb, scale,
-            dtype_code(q.dtype), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-            sp.member.data_ptr(), sp.rows.data_ptr(), sp.rows.numel(), sp.table.data_ptr(), sp.table.numel(),
-            sp.split_len, stream_handle(device),
+            dtype_code(q.dtype), None, None, None, None, None, None, 0,
+            *_prefix_call(shared_prefix, rows, block_tables),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), stream_handle(device),
         )
         check(rc, "rlt_paged_decode_shared_prefix")
         return out

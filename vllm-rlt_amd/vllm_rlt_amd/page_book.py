@@ -67,6 +67,9 @@ class Allocation:
     written: list
     transfer_leases: set = field(default_factory=set)
     release_requested: bool = False
+    # Leading pages of every plane taken from the prefix cache at admission
+    # (shared read-only with other requests; fixed for the request's life).
+    prefix_pages: int = 0
 
 
 @dataclass(frozen=True, eq=False)
@@ -90,8 +93,8 @@ class PreparedKVBatch:
     writable: bool
     cu_seqlens_q: torch.Tensor | None = None
     max_seqlen_q: int = 1
-    # Rows reading the same prefix pages, when the manager shares those reads
-    # (an ops.SharedPrefix; no counterpart in the reference's batch).
+    # Rows grouped by the prefix-cache pages they read, when the manager shares
+    # those reads (an ops.PrefixGroups; no counterpart in the reference's batch).
     shared_prefix: Any = None
 
 
@@ -289,7 +292,7 @@ class KVPageBook:
         )
         cached = len(prefix) * self.block_size
         written = [[WrittenPrefix(prefix=cached) for _ in range(self.num_layers)] for _ in range(self.storage_depths)]
-        self._allocations[request_id] = Allocation(int(max_tokens), tables, written)
+        self._allocations[request_id] = Allocation(int(max_tokens), tables, written, prefix_pages=len(prefix))
         self.prefix_queries += 1
         self.prefix_hits += cached
         return True

@@ -107,23 +107,24 @@ class HipPagedAttention:
         return self.reserve(ops.decode_workspace_bytes(rows, num_q_heads, num_kv_heads, self.head_dim))
 
     def __call__(self, q, key_cache, value_cache, block_tables, context_lengths, shared_prefix=None):
-        """Decode attention; `shared_prefix` (an ops.SharedPrefix, beyond the
-        reference's signature) reads rows' aliased prefix pages once."""
+        """Decode attention; `shared_prefix` (an ops.PrefixGroups, beyond the
+        reference's signature) reads each group's aliased prefix pages once."""
         workspace = self.reserve_decode(q.shape[0], q.shape[1], key_cache.shape[2]) if q.shape[0] else None
         return ops.paged_decode(
             q, key_cache, value_cache, block_tables, context_lengths, workspace=workspace, shared_prefix=shared_prefix
         )
 
     def decode_append(self, q, key_cache, value_cache, block_tables, context_lengths, k_new, v_new, write_blocks,
-                      write_offsets, n_write=None):
+                      write_offsets, n_write=None, shared_prefix=None):
         """Append rows' new K/V, then decode attention, in one launch (beyond the reference's interface).
 
         The caller guarantees that no row reads a slot another row writes.
+        `shared_prefix` as for __call__.
         """
         workspace = self.reserve_decode(q.shape[0], q.shape[1], key_cache.shape[2]) if q.shape[0] else None
         return ops.paged_decode_append(
             q, key_cache, value_cache, block_tables, context_lengths, k_new, v_new, write_blocks, write_offsets,
-            n_write=n_write, workspace=workspace,
+            n_write=n_write, workspace=workspace, shared_prefix=shared_prefix,
         )
 
     def prefill(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q, max_seqlen_q):
