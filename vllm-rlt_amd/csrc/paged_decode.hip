@@ -704,8 +704,10 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 constexpr int kPrefixBK = 32;   // keys per tile
 constexpr float kPrefixRescale = 8.f;
 
+// Two waves per SIMD (at most 256 registers a lane, none spilled): one launch
+// round for 512 workgroups, where the latency-bound pass otherwise takes two.
 template <typename T, int G>
-__global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void shared_prefix_kernel(DecodeArgs a) {
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   constexpr int D = 128, KSTEPS = D / 16, DTILES = D / 32;
@@ -746,30 +748,13 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
   uint16_t* const k_lds = tiles + kh * (KTILE + VTILE);
   uint16_t* const v_lds = k_lds + KTILE;
 
-  // This lane's query: (member qi / G of group g, q head h * G + qi % G).
-  const int qi = qblock * 64 + qw * 32 + col;
-  const bool listed = qi < n_members * G;
-  const int r = a.pg_members[rec[kGroupMember0] + (listed ? qi / G : 0)];
-  const int j = listed ? qi % G : 0;
-  bool mine = false;
-  if (listed && r >= 0 && r < a.n_rows && a.pg_row_group[r] == g) {
-    int split_len, ns;
-    split_plan(row_length(a, r), &split_len, &ns);
-    mine = prefix_takes(a, r, sp, split_len, ns);
-  }
-  if (!__syncthreads_or(mine)) return;
-  const int rq = mine ? r : 0;
-
-  // q as the B operand: lane (col, half) holds dims 16ks + 8half .. + 7.
-  u32x4 qb[KSTEPS];
-  {
-    const T* qrow = static_cast<const T*>(a.q) + rq * a.q_row + static_cast<int64_t>(h * G + j) * a.q_head;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
-  }
+  // An item past the group's whole splits (the host's item count may cover
+  // more query blocks than there are) has nothing to do.
+  if (static_cast<int64_t>(sp + 1) * S > static_cast<int64_t>(rec[kGroupPages]) * a.page) return;
 
   // Staging: within a key half, thread t (of 128) moves 16-byte chunk
   // (t + 128i) % 16 of tile row (t + 128i) / 16, i = 0..3, for K and for V.
+  // The split lies inside the group's pages, so every page id read is one of them.
   const int32_t* group_pages = a.pg_pages + rec[kGroupPage0];
   const int ntiles = S / kPrefixBK / 2;  // per key half
   const int key0 = sp * S + kh * ntiles * kPrefixBK;
@@ -790,6 +775,35 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
       vr[i] = load_page(reinterpret_cast<const u32x4*>(vbase + off));
     }
   };
+  // The first two tiles depend on the group alone: their loads go out before
+  // the membership checks below, whose chain of dependent reads they overlap.
+  // (S = 256 << k keys, so each key half has at least two tiles.)
+  load_tile(0, kreg[0], vreg[0]);
+  load_tile(1, kreg[1], vreg[1]);
+
+  // This lane's query: (member qi / G of group g, q head h * G + qi % G).
+  const int qi = qblock * 64 + qw * 32 + col;
+  const bool listed = qi < n_members * G;
+  const int r = a.pg_members[rec[kGroupMember0] + (listed ? qi / G : 0)];
+  const int j = listed ? qi % G : 0;
+  const bool row_ok = listed && r >= 0 && r < a.n_rows;
+  const int rq = row_ok ? r : 0;
+  // q as the B operand (lane (col, half) holds dims 16ks + 8half .. + 7),
+  // loaded for every listed row before its membership is known.
+  u32x4 qb[KSTEPS];
+  {
+    const T* qrow = static_cast<const T*>(a.q) + rq * a.q_row + static_cast<int64_t>(h * G + j) * a.q_head;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
+  }
+  bool mine = false;
+  if (row_ok && a.pg_row_group[r] == g) {
+    int split_len, ns;
+    split_plan(row_length(a, r), &split_len, &ns);
+    mine = prefix_takes(a, r, sp, split_len, ns);
+  }
+  if (!__syncthreads_or(mine)) return;
+
   auto store_tile = [&](const u32x4 (&kr)[4], const u32x4 (&vr)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -862,8 +876,6 @@ __global__ __launch_bounds__(256) void shared_prefix_kernel(DecodeArgs a) {
     }
   };
   // S = 256 << k keys, so each key half has an even tile count.
-  load_tile(0, kreg[0], vreg[0]);
-  load_tile(1, kreg[1], vreg[1]);
   for (int t = 0; t < ntiles; t += 2) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
