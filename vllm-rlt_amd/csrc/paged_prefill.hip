@@ -534,7 +534,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // k-steps, and each MFMA's wait then covers reads it does not use.  P^T of
   // k-step ks is rounded to T one k-step early and added to the row sum
   // (v_dot2 against ones) after that step's MFMAs.
-  constexpr int kStreamAhead = 3;
+  constexpr int kStreamAhead = 4;
   auto mfma_phase = [&](auto pv_tag, auto s_tag, int b_pv, int b_s, f32x16 (&sacc)[2], bool rescale, float corr)
                         __attribute__((always_inline)) {
     constexpr bool PV = decltype(pv_tag)::value, S = decltype(s_tag)::value;
