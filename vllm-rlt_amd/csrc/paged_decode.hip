@@ -107,6 +107,7 @@ struct DecodeArgs {
   int64_t o_row, o_head, o_dim;
   float* ws_acc;  // [rows][hkv][kMaxSplits][G][D]
   float2* ws_ml;  // [rows][hkv][kMaxSplits][G]  (max in log2 units, sum)
+  uint8_t* ws_taken;  // [rows][kMaxSplits]: split taken by the prefix pass (written by it each launch)
   int n_rows, hkv, hq, d, page;
   int xcd_groups;  // > 0: XCD-affine schedule over this many (split, head block) groups
   int64_t num_blocks;
@@ -164,25 +165,42 @@ __device__ __forceinline__ const int32_t* group_record(const DecodeArgs& a, int 
   return ok ? rec : nullptr;
 }
 
-// True when split sp of row r (split_len tokens, ns splits) is computed by
-// shared_prefix_kernel rather than by the split pass.  Both kernels evaluate
-// this same predicate, so every split is produced exactly once.  The row must
-// be in a group that uses its split length; the split must lie inside the
-// group's pages and leave at least one split of the row to the split pass (so
-// the row goes through the merge), and the row's table must hold exactly the
-// group's pages there.  All of it depends on the row and its own group only.
-__device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
-  if (!a.pg_row_group) return false;
+// The record of row r's group when split sp of the row (split_len tokens, ns
+// splits) can go to the prefix pass: the group uses the row's split length, and
+// the split lies inside the group's pages, within the prefix pass's items
+// (splits below kMaxSplits - 1), and is not the row's last split (so the row
+// goes through the merge).  Null otherwise.
+__device__ __forceinline__ const int32_t* prefix_candidate(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
+  if (!a.pg_row_group) return nullptr;
   const int32_t* rec = group_record(a, a.pg_row_group[r]);
-  if (!rec || rec[kGroupSplit] != split_len) return false;
+  if (!rec || rec[kGroupSplit] != split_len) return nullptr;
   const int64_t covered = static_cast<int64_t>(rec[kGroupPages]) * a.page / split_len;
-  if (sp >= covered || sp >= ns - 1) return false;
+  if (sp >= covered || sp >= ns - 1 || sp >= kMaxSplits - 1) return nullptr;
+  return rec;
+}
+
+// True when split sp of row r is computed by shared_prefix_kernel rather than
+// by the split pass: it is a candidate and the row's table holds exactly the
+// group's pages there.  All of it depends on the row and its own group only.
+// The prefix pass evaluates this for every (member row, candidate split) of
+// every group and records the answer in ws_taken; the split pass, which runs
+// after it, reads the record (prefix_taken) instead of comparing the pages
+// again, so every split is produced exactly once.
+__device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
+  const int32_t* rec = prefix_candidate(a, r, sp, split_len, ns);
+  if (!rec) return false;
   const int pages = split_len / a.page;
   const int32_t* trow = a.tables + static_cast<int64_t>(r) * a.table_stride + sp * pages;
   const int32_t* shared = a.pg_pages + rec[kGroupPage0] + sp * pages;
   bool same = true;
   for (int i = 0; i < pages; ++i) same &= trow[i] == shared[i];
   return same;
+}
+
+// The split pass's side of prefix_takes: the prefix pass's record for a
+// candidate split.
+__device__ __forceinline__ bool prefix_taken(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
+  return prefix_candidate(a, r, sp, split_len, ns) && a.ws_taken[static_cast<int64_t>(r) * kMaxSplits + sp] != 0;
 }
 
 // K/V page reads: each byte is read once per launch.
@@ -615,7 +633,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int len = uniform(row_length(a, r));
     int split_len, ns;
     split_plan(len, &split_len, &ns);
-    if (sp < ns && !(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
+    if (sp < ns && !(PREFIX && uniform(prefix_taken(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
   } else {
     // Packed schedule (any head count): the compact list of rows x splits x
     // kv heads, kv head innermost, walked in grid-stride order.
@@ -630,7 +648,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       const int len = uniform(row_length(a, r));
       int split_len, ns;
       split_plan(len, &split_len, &ns);
-      if (!(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
+      if (!(PREFIX && uniform(prefix_taken(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
     }
   }
 }
@@ -801,6 +819,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     int split_len, ns;
     split_plan(row_length(a, r), &split_len, &ns);
     mine = prefix_takes(a, r, sp, split_len, ns);
+    // The record the split pass reads: every (member, candidate split) pair is
+    // in exactly one item of its group, whose lanes of that member (one per
+    // q head of the KV head, for every KV head) all write the same value.
+    if (h == 0 && j == 0 && prefix_candidate(a, r, sp, split_len, ns))
+      a.ws_taken[static_cast<int64_t>(r) * kMaxSplits + sp] = mine ? 1 : 0;
   }
   if (!__syncthreads_or(mine)) return;
 
@@ -1166,9 +1189,9 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
 
 int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Workspace layout: acc partials | (max, sum) partials.
+// Workspace layout: acc partials | (max, sum) partials | prefix-taken bytes.
 struct WorkspaceLayout {
-  int64_t acc, ml, total;
+  int64_t acc, ml, taken, total;
 };
 WorkspaceLayout workspace_layout(int64_t rows, int64_t hq, int64_t hkv, int64_t d) {
   rows = std::min<int64_t>(rows, kMaxRowsPerLaunch);
@@ -1176,7 +1199,8 @@ WorkspaceLayout workspace_layout(int64_t rows, int64_t hq, int64_t hkv, int64_t 
   WorkspaceLayout w{};
   w.acc = 0;
   w.ml = round256(slots * d * static_cast<int64_t>(sizeof(float)));
-  w.total = w.ml + round256(slots * static_cast<int64_t>(sizeof(float2)));
+  w.taken = w.ml + round256(slots * static_cast<int64_t>(sizeof(float2)));
+  w.total = w.taken + round256(rows * kMaxSplits);
   return w;
 }
 
@@ -1257,6 +1281,7 @@ int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
   char* ws = static_cast<char*>(workspace);
   a.ws_acc = reinterpret_cast<float*>(ws + layout.acc);
   a.ws_ml = reinterpret_cast<float2*>(ws + layout.ml);
+  a.ws_taken = reinterpret_cast<uint8_t*>(ws + layout.taken);
   a.hkv = static_cast<int>(num_kv_heads);
   a.hq = static_cast<int>(num_q_heads);
   a.d = static_cast<int>(head_dim);
