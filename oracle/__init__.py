@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (vllm-rlt_amd/) imports,
 links or runs this package.  Only tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg may use it, and only as the checker (or, in the
-bench, as the timed CPU baseline) -- never as the thing measured on the GPU.
+bench.py's parity spot checks and cpu_baseline leg may use it: to check
+results (or, in the bench, as the timed CPU baseline) -- never as the thing
+measured on the GPU.
 
 Contents and what pins each function (see tests/test_oracle.py):
 
