@@ -11,6 +11,9 @@ launch paths only large inputs reach (GPU).
   prefix (512 pages) shared read-only by every table, page ids placed past
   element 2**32 of the pool (tests/test_attention_64bit.py:16-30,
   tests/test_prefix_growth.py:47-64), through the shared-prefix entry point.
+* Prefix caching under LAST-EXITED (every plane its own 2048-token prefix,
+  contexts U[4096, 8192], mixed depths): one fused append + decode launch with
+  the step's prefix groups; all four planes' prefix pages stay bit-identical.
 * More than 8192 decode rows (the entry point's per-launch row chunking) and
   a prefill whose block tables are wider than 4096 pages (the MFMA variant
   that reads page ids from the table instead of staging them in LDS).
@@ -278,4 +281,75 @@ def test_aliased_prefix_decode_full_size_64bit_pages():
     for r in range(rows):
         ref = _fp32_reference(q[r], key_cache[:, 0], value_cache[:, 0], tables_dev[r], lengths[r], scale)
         torch.testing.assert_close(out[r].float(), ref, **BF16_TOL)
+    torch.testing.assert_close(out, plain, **BF16_TOL)
+
+
+def test_last_exited_prefix_groups_full_size():
+    """Prefix caching under the reference's own semantics at the bench shape: 64
+    requests, contexts U[4096, 8192], four LAST-EXITED planes, each plane's tables
+    beginning with that plane's 2048-token prefix, every request at a depth drawn
+    from U{1..4}; the fused append with the step's prefix groups."""
+    from vllm_rlt_amd import ops
+
+    _need_free(12)
+    g = torch.Generator().manual_seed(7007)
+    rows, planes, prefix_pages = 64, 4, 2048 // PAGE
+    contexts = torch.randint(4096, 8193, (rows,), generator=g).tolist()
+    depths = torch.randint(0, planes, (rows,), generator=g).tolist()
+    lengths = [c + 1 for c in contexts]
+    own = [math.ceil(n / PAGE) - prefix_pages for n in lengths]
+    nb = planes * prefix_pages + planes * sum(own) + 8
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    prefixes = perm[: planes * prefix_pages].view(planes, prefix_pages)
+    used = planes * prefix_pages
+    width = max(own) + prefix_pages
+    plane_tables = torch.full((rows, planes, width), -1, dtype=torch.int32)
+    for r in range(rows):
+        for p in range(planes):
+            plane_tables[r, p, :prefix_pages] = prefixes[p]
+            plane_tables[r, p, prefix_pages : prefix_pages + own[r]] = perm[used : used + own[r]]
+            used += own[r]
+    tables = plane_tables[torch.arange(rows), torch.tensor(depths)].contiguous()  # depth-resolved rows
+    dev = torch.device("cuda")
+    shape = (nb, 1, PAGE, HEADS, HEAD_DIM)
+    key_cache = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    value_cache = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(7008)
+    for pool in (key_cache, value_cache):
+        flat = pool.view(-1)
+        for start in range(0, flat.numel(), 1 << 28):
+            flat[start : start + (1 << 28)].normal_(generator=gen)
+    q = torch.randn((rows, HEADS, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    k_new = torch.randn((rows, HEADS, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((rows, HEADS, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    blocks = torch.tensor([int(tables[r, c // PAGE]) for r, c in enumerate(contexts)], dtype=torch.int64)
+    offsets = torch.tensor([c % PAGE for c in contexts], dtype=torch.int64)
+    prefix_dev = prefixes.reshape(-1).long().to(dev)
+    snapshot = key_cache[prefix_dev].clone(), value_cache[prefix_dev].clone()
+    groups = ops.prefix_groups([prefixes[d].tolist() for d in depths], lengths, PAGE, 1, dev)
+    assert groups.n_groups == len(set(depths)) and groups.n_members == rows
+    print(f"[LAST-EXITED prefix groups full size] {groups.n_groups} groups, {nb} pages", flush=True)
+
+    tables_dev, lengths_dev = tables.to(dev), torch.tensor(lengths, dtype=torch.int32, device=dev)
+    out = ops.paged_decode_append(
+        q, key_cache[:, 0], value_cache[:, 0], tables_dev, lengths_dev, k_new, v_new, blocks.to(dev),
+        offsets.to(dev), shared_prefix=groups,
+    )
+    torch.cuda.synchronize()
+    # Every plane's prefix pages are read-only: bit-identical after the fused launch.
+    assert torch.equal(key_cache[prefix_dev], snapshot[0]) and torch.equal(value_cache[prefix_dev], snapshot[1])
+    # The appended slots hold the new tokens exactly.
+    assert torch.equal(key_cache[blocks.to(dev), 0, offsets.to(dev)], k_new)
+    assert torch.equal(value_cache[blocks.to(dev), 0, offsets.to(dev)], v_new)
+    # Sampled rows (one per plane at least) against the CPU oracle on host copies of their pages.
+    sample = sorted({0, rows - 1, *[depths.index(p) for p in set(depths)]})
+    hk, hv, small = _host_pages(key_cache[:, 0], value_cache[:, 0], tables[sample], [lengths[r] for r in sample])
+    expect = paged_attention_cpu(q[sample].cpu(), hk, hv, small, torch.tensor([lengths[r] for r in sample], dtype=torch.int32))
+    torch.testing.assert_close(out[sample].cpu(), expect, **BF16_TOL)
+    # Every row against a dense fp32 device reference, and against the plain decode.
+    scale = HEAD_DIM**-0.5
+    for r in range(rows):
+        ref = _fp32_reference(q[r], key_cache[:, 0], value_cache[:, 0], tables_dev[r], lengths[r], scale)
+        torch.testing.assert_close(out[r].float(), ref, **BF16_TOL)
+    plain = ops.paged_decode(q, key_cache[:, 0], value_cache[:, 0], tables_dev, lengths_dev)
     torch.testing.assert_close(out, plain, **BF16_TOL)
