@@ -93,3 +93,17 @@ def test_no_groups_without_a_whole_split_of_shared_pages():
     assert ops.prefix_group_layout([list(range(20))], [0], 16, 1) is None  # empty row
     with pytest.raises(ValueError, match="one length per row"):
         ops.prefix_group_layout([()], [1, 2], 16, 1)
+
+
+def test_rows_join_a_group_by_its_first_and_last_page_and_count():
+    # Grouping costs O(1) per row: a row whose pages agree with the group's at
+    # the ends joins it (the device compares every page before taking a split,
+    # so a differing middle page only sends that split to the split pass).
+    a = list(range(100, 140))
+    b = a[:10] + [999] + a[11:]
+    c = a[:31] + [7] + a[32:]  # differs at the last page of the 32-page cut
+    layout = ops.prefix_group_layout([a, b, c], [1000, 1000, 1000], 16, 1)
+    row_group, records, _, members, pages = sections(layout, 3)
+    assert row_group.tolist() == [0, 0, 1]
+    assert pages[:32].tolist() == a[:32]  # the first member's list
+    assert members.tolist() == [0, 1, 2]

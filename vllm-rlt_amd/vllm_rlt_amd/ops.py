@@ -313,39 +313,47 @@ def prefix_group_layout(row_pages, lengths, page: int, group_size: int):
     or None: the row reads no shared prefix).  Rows group by those pages cut
     to whole splits of their own split length (decode_split_len of their
     length), and by that split length; rows whose pages cover no whole split
-    stay out.  group_size is the number of q heads per KV head (a larger value
-    only adds empty work items; the hint serves calls up to it).  Groups appear
-    in first-member order and list members in batch order, so the layout is a
-    function of the rows alone.
+    stay out.  A group's page list is its first member's; rows join a group by
+    its first and last page and page count, so building the layout costs
+    O(1) per row beyond the group lists (the device compares every page of a
+    member's split before it takes it, so a row whose middle pages differ only
+    reads its own pages in the split pass).  group_size is the number of q
+    heads per KV head (a larger value only adds empty work items; the hint
+    serves calls up to it).  Groups appear in first-member order and list
+    members in batch order, so the layout is a function of the rows alone.
     """
     n_rows = len(row_pages)
     if len(lengths) != n_rows:
         raise ValueError("one length per row")
-    groups: dict = {}
+    groups: dict = {}  # (first page, last page, pages, split length) -> (group, page list)
     row_group = np.full(n_rows, -1, dtype=np.int32)
     for r, (pages, n) in enumerate(zip(row_pages, lengths)):
         if pages is None or not len(pages) or int(n) <= 0:
             continue
         split = decode_split_len(int(n))
-        covered = len(pages) * page // split
-        if covered == 0:
+        cut = len(pages) * page // split * split // page
+        if cut == 0:
             continue
-        key = (tuple(int(b) for b in pages[: covered * split // page]), split)
-        row_group[r] = groups.setdefault(key, len(groups))
+        key = (int(pages[0]), int(pages[cut - 1]), cut, split)
+        entry = groups.get(key)
+        if entry is None:
+            entry = groups[key] = (len(groups), pages[:cut])
+        row_group[r] = entry[0]
     if not groups:
         return None
     members = [[] for _ in groups]
     for r in np.nonzero(row_group >= 0)[0]:
         members[row_group[r]].append(int(r))
-    records, item_start, pages_flat = [], [0], []
-    member0 = 0
-    for (pages, split), g in groups.items():
+    records, item_start, page_lists = [], [0], []
+    member0 = page0 = 0
+    for (_, _, cut, split), (g, pages) in groups.items():
         count = len(members[g])
-        splits = min(len(pages) * page // split, DECODE_MAX_SPLITS - 1)
-        records.append((member0, count, len(pages_flat), len(pages), split))
+        splits = min(cut * page // split, DECODE_MAX_SPLITS - 1)
+        records.append((member0, count, page0, cut, split))
         item_start.append(item_start[-1] + splits * (-(-count * group_size // 64)))
-        pages_flat.extend(pages)
+        page_lists.append(np.asarray(pages, dtype=np.int32))
         member0 += count
+        page0 += cut
     flat_members = [r for m in members for r in m]
     hint = np.concatenate(
         [
@@ -353,10 +361,10 @@ def prefix_group_layout(row_pages, lengths, page: int, group_size: int):
             np.asarray(records, dtype=np.int32).reshape(-1),
             np.asarray(item_start, dtype=np.int32),
             np.asarray(flat_members, dtype=np.int32),
-            np.asarray(pages_flat, dtype=np.int32),
+            *page_lists,
         ]
     ).astype(np.int32)
-    return hint, len(groups), len(flat_members), len(pages_flat), item_start[-1], int(group_size)
+    return hint, len(groups), len(flat_members), page0, item_start[-1], int(group_size)
 
 
 def prefix_groups(row_pages, lengths, page: int, group_size: int, device) -> PrefixGroups | None:
