@@ -100,7 +100,10 @@ def test_prefix_keys_are_chained_sha256_of_full_pages():
     tokens = [5, 6, 7, 8, 9, 10, 11, 12, 13]
     first = hashlib.sha256(struct.pack("<4q", 5, 6, 7, 8)).digest()
     second = hashlib.sha256(first + struct.pack("<4q", 9, 10, 11, 12)).digest()
-    assert list(c._prefix_keys(tokens)) == [first, second]
+    assert list(c._index.keys(tokens)) == [first, second]
+    # A partial last page has no key; a prefix of the tokens shares its keys.
+    assert list(c._index.keys(tokens[:7])) == [first]
+    assert list(c._index.keys(tokens[:3])) == []
 
 
 def test_prefix_publication_needs_every_plane_and_layer_written():

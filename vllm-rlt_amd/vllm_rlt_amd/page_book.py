@@ -14,7 +14,6 @@ per loop depth, SHARED a single plane every depth writes.
 from __future__ import annotations
 
 import hashlib
-import struct
 from collections import OrderedDict
 from collections.abc import Sequence
 from dataclasses import dataclass, field
@@ -114,6 +113,122 @@ class BatchPlan:
     writable: bool
 
 
+class _PagePool:
+    """Physical pages with reference counts; unreferenced pages wait on a LIFO stack.
+
+    The stack starts as [n-1, ..., 1, 0], so the first pages handed out are
+    0, 1, 2, ... (kv_cache_manager.py:137, :142).  A page is held once per
+    request table that lists it and once per prefix-index entry that names it.
+    """
+
+    __slots__ = ("free", "refs")
+
+    def __init__(self, count: int):
+        self.free = list(range(count - 1, -1, -1))
+        self.refs = [0] * count
+
+    def retain(self, pages) -> None:
+        refs = self.refs
+        for b in pages:
+            refs[b] += 1
+
+    def release(self, pages) -> None:
+        """Drop one hold per page, in the order given; a page left unheld is pushed (:175-180)."""
+        refs, free = self.refs, self.free
+        for b in pages:
+            refs[b] -= 1
+            if refs[b] == 0:
+                free.append(b)
+            elif refs[b] < 0:
+                raise AssertionError(f"page {b} released more often than held")
+
+    def take(self, count: int) -> list:
+        """The top `count` pages of the stack, top first, each now held once."""
+        cut = len(self.free) - count
+        pages = self.free[cut:][::-1]
+        del self.free[cut:]
+        for b in pages:
+            if self.refs[b]:
+                raise AssertionError(f"free page {b} is still held")
+            self.refs[b] = 1
+        return pages
+
+
+class _PrefixIndex:
+    """Cached full prompt pages, least recently used first (kv_cache_manager.py:194-251).
+
+    A key names a whole token prefix up to the end of one page: the sha256 of
+    the previous page's key followed by the page's tokens as little-endian
+    int64, starting from the empty key.  A value holds the page's physical id
+    in every storage plane.  The index keeps one pool hold on each of them.
+    """
+
+    __slots__ = ("page", "entries")
+
+    def __init__(self, page_tokens: int):
+        self.page = page_tokens
+        self.entries: OrderedDict = OrderedDict()
+
+    def keys(self, tokens):
+        """Keys of the full pages of `tokens`, computed lazily in page order."""
+        step = self.page
+        whole = len(tokens) - len(tokens) % step
+        if not whole:
+            return
+        data = memoryview(np.asarray(tokens[:whole], dtype="<i8").tobytes())
+        key = b""
+        for start in range(0, whole * 8, step * 8):
+            h = hashlib.sha256(key)
+            h.update(data[start : start + step * 8])
+            key = h.digest()
+            yield key
+
+    def match(self, tokens) -> tuple:
+        """The cached pages of the longest indexed run of `tokens`' full pages, marked recently used."""
+        run = []
+        for key in self.keys(tokens):
+            pages = self.entries.get(key)
+            if pages is None:
+                break
+            self.entries.move_to_end(key)
+            run.append(pages)
+        return tuple(run)
+
+    def add_run(self, tokens, tables, pool: _PagePool) -> None:
+        """Index every full page of `tokens` not indexed yet; page i is (table[i] for each plane)."""
+        for index, key in enumerate(self.keys(tokens)):
+            if key not in self.entries:
+                pages = tuple(table[index] for table in tables)
+                pool.retain(pages)
+                self.entries[key] = pages
+
+    def evict_oldest(self):
+        """Remove the least recently used entry and return its pages (None when empty)."""
+        if not self.entries:
+            return None
+        return self.entries.popitem(last=False)[1]
+
+    def reclaimable(self, pool: _PagePool) -> int:
+        """Indexed pages no request holds (the index's hold is their last)."""
+        return sum(1 for pages in self.entries.values() for b in pages if pool.refs[b] == 1)
+
+
+@dataclass
+class _DeferredPublish:
+    """A publication waiting for the device writes behind `event` (kv_cache_manager.py:201-209)."""
+
+    request_id: str
+    allocation: Allocation
+    tokens: tuple
+    length: int
+    event: Any
+
+
+def _widen(tables: tuple, fresh: list, per_plane: int) -> tuple:
+    """Plane d's table followed by fresh[d * per_plane:(d + 1) * per_plane]."""
+    return tuple(table + tuple(fresh[d * per_plane : (d + 1) * per_plane]) for d, table in enumerate(tables))
+
+
 class KVPageBook:
     """Page allocator, prefix cache and per-position validity of a paged KV pool."""
 
@@ -151,20 +266,31 @@ class KVPageBook:
         self.enable_prefix_caching = enable_prefix_caching
         self.incremental_allocation = incremental_allocation
         self.watermark_blocks = int(watermark_ratio * self.num_blocks)
-        # LIFO free stack whose first pops are 0, 1, 2, ...
-        self._free_blocks = list(range(self.num_blocks - 1, -1, -1))
-        self._refs = [0] * self.num_blocks
+        self._pool = _PagePool(self.num_blocks)
+        self._index = _PrefixIndex(self.block_size)
+        self._deferred: list = []
         self._allocations: dict[str, Allocation] = {}
-        self._prefixes: OrderedDict = OrderedDict()
-        self._pending_prefixes: list = []
         self.prefix_hits = self.prefix_queries = 0
 
     # ------------------------------------------------------------------ pool
+    # The page holds, free stack and prefix entries under the names the
+    # reference's scheduler and tests read (scheduler.py:207, test_cdb_runtime.py:176).
+    @property
+    def _refs(self) -> list:
+        return self._pool.refs
+
+    @property
+    def _free_blocks(self) -> list:
+        return self._pool.free
+
+    @property
+    def _prefixes(self) -> OrderedDict:
+        return self._index.entries
+
     @property
     def num_free_blocks(self) -> int:
         """Free pages plus cached prefix pages only the cache still holds (:149-153)."""
-        reclaimable = sum(1 for pages in self._prefixes.values() for b in pages if self._refs[b] == 1)
-        return len(self._free_blocks) + reclaimable
+        return len(self._pool.free) + self._index.reclaimable(self._pool)
 
     @property
     def num_used_blocks(self) -> int:
@@ -176,94 +302,62 @@ class KVPageBook:
             raise ValueError("max_tokens must be a positive integer")
         return -(-max_tokens // self.block_size) * self.storage_depths
 
-    def _drop_refs(self, blocks) -> None:
-        """Release one reference per page; unreferenced pages return to the free stack (:175-180)."""
-        for b in blocks:
-            left = self._refs[b] - 1
-            assert left >= 0
-            self._refs[b] = left
-            if left == 0:
-                self._free_blocks.append(b)
-
-    def _claim(self, count: int):
-        """Pop count pages, evicting least-recently-used prefixes when short (:182-192)."""
-        while len(self._free_blocks) < count and self._prefixes:
-            _, evicted = self._prefixes.popitem(last=False)
-            self._drop_refs(evicted)
-        if len(self._free_blocks) < count:
-            return None
-        claimed = [self._free_blocks.pop() for _ in range(count)]
-        for b in claimed:
-            assert self._refs[b] == 0
-            self._refs[b] = 1
-        return claimed
+    def _take_pages(self, count: int):
+        """`count` fresh pages, evicting least recently used prefixes while short; None if
+        even an empty index leaves too few (:182-192)."""
+        pool = self._pool
+        while len(pool.free) < count:
+            evicted = self._index.evict_oldest()
+            if evicted is None:
+                return None
+            pool.release(evicted)
+        return pool.take(count)
 
     # --------------------------------------------------------- prefix cache
-    def _prefix_keys(self, tokens):
-        """Chained sha256 digest of every full page of tokens (:194-199)."""
-        digest = b""
-        page = self.block_size
-        for start in range(0, len(tokens) - len(tokens) % page, page):
-            chunk = tokens[start : start + page]
-            digest = hashlib.sha256(digest + struct.pack(f"<{len(chunk)}q", *chunk)).digest()
-            yield digest
-
     def poll_prefixes(self) -> None:
-        """Publish deferred prefixes whose completion event has fired (:201-209)."""
-        waiting, self._pending_prefixes = self._pending_prefixes, []
-        for request_id, allocation, tokens, length, event in waiting:
-            if self._allocations.get(request_id) is not allocation:
+        """Publish deferred prefixes whose completion event has fired, in arrival order (:201-209).
+
+        A request freed (or freed and re-admitted) since it asked is dropped.
+        """
+        waiting, self._deferred = self._deferred, []
+        for item in waiting:
+            if self._allocations.get(item.request_id) is not item.allocation:
                 continue
-            if event is not None and not event.query():
-                self._pending_prefixes.append((request_id, allocation, tokens, length, event))
-                continue
-            self.publish_prefix(request_id, tokens, length)
+            if item.event is not None and not item.event.query():
+                self._deferred.append(item)
+            else:
+                self.publish_prefix(item.request_id, item.tokens, item.length)
 
     def publish_prefix(self, request_id, tokens, length, event=None) -> None:
         """Index full prompt pages written at every depth and layer for reuse (:211-238).
 
-        At least the last prompt token is left out (its hidden state is not
-        cached), and publication stops at the first page some (plane, layer)
-        has not fully written.
+        The last prompt token is never published (its hidden state is not
+        cached), and only pages every (plane, layer) has written contiguously
+        from position 0 qualify.  With an event, publication waits for it.
         """
         if not self.enable_prefix_caching:
             return
         allocation = self._get_allocation(request_id)
         if event is not None:
-            self._pending_prefixes.append((request_id, allocation, tuple(tokens), length, event))
+            self._deferred.append(_DeferredPublish(request_id, allocation, tuple(tokens), length, event))
             return
-        limit = min(length, len(tokens) - 1)
-        for index, key in enumerate(self._prefix_keys(tokens[:limit])):
-            if key in self._prefixes:
-                continue
-            end = (index + 1) * self.block_size
-            if any(w.prefix < end for plane in allocation.written for w in plane):
-                break
-            pages = tuple(table[index] for table in allocation.block_tables)
-            for b in pages:
-                self._refs[b] += 1
-            self._prefixes[key] = pages
+        publishable = tokens[: min(length, len(tokens) - 1)]
+        written = min(w.prefix for plane in allocation.written for w in plane)
+        self._index.add_run(publishable[: written - written % self.block_size], allocation.block_tables, self._pool)
 
     def lookup_prefix(self, tokens) -> tuple:
         """Longest cached run of full pages of tokens[:-1], refreshed as recently used (:240-251)."""
         if not self.enable_prefix_caching:
             return ()
         self.poll_prefixes()
-        hits = []
-        for key in self._prefix_keys(tokens[:-1]):
-            pages = self._prefixes.get(key)
-            if pages is None:
-                break
-            self._prefixes.move_to_end(key)
-            hits.append(pages)
-        return tuple(hits)
+        return self._index.match(tokens[:-1])
 
     # ----------------------------------------------------------- allocation
     def allocate(self, request_id: str, max_tokens: int, *, initial_tokens=None, prefix=()) -> bool:
         """Reserve capacity and pages for the initial frontier (:253-293).
 
-        Plane d's table is the shared prefix pages' plane-d entries followed by
-        fresh pages claimed[d * tail:(d + 1) * tail].
+        Plane d's table is the prefix pages' plane-d entries followed by that
+        plane's share of the fresh pages.  On failure nothing stays held.
         """
         if not isinstance(request_id, str) or not request_id:
             raise ValueError("request_id must be a nonempty string")
@@ -278,21 +372,20 @@ class KVPageBook:
         pages = -(-frontier // self.block_size)
         if len(prefix) > pages:
             raise ValueError("prefix exceeds initial KV frontier")
-        shared = [b for group in prefix for b in group]
-        for b in shared:
-            self._refs[b] += 1
+        # Hold the prefix pages first so that making room cannot evict them.
+        aliased = [b for entry in prefix for b in entry]
+        self._pool.retain(aliased)
         tail = pages - len(prefix)
-        fresh = self._claim(tail * self.storage_depths)
+        fresh = self._take_pages(tail * self.storage_depths)
         if fresh is None:
-            self._drop_refs(shared)
+            self._pool.release(aliased)
             return False
-        tables = tuple(
-            tuple(group[plane] for group in prefix) + tuple(fresh[plane * tail : (plane + 1) * tail])
-            for plane in range(self.storage_depths)
-        )
+        heads = tuple(tuple(entry[d] for entry in prefix) for d in range(self.storage_depths))
         cached = len(prefix) * self.block_size
         written = [[WrittenPrefix(prefix=cached) for _ in range(self.num_layers)] for _ in range(self.storage_depths)]
-        self._allocations[request_id] = Allocation(int(max_tokens), tables, written, prefix_pages=len(prefix))
+        self._allocations[request_id] = Allocation(
+            int(max_tokens), _widen(heads, fresh, tail), written, prefix_pages=len(prefix)
+        )
         self.prefix_queries += 1
         self.prefix_hits += cached
         return True
@@ -305,17 +398,17 @@ class KVPageBook:
         extra = -(-tokens // self.block_size) - len(allocation.block_tables[0])
         if extra <= 0:
             return True
-        fresh = self._claim(extra * self.storage_depths)
+        fresh = self._take_pages(extra * self.storage_depths)
         if fresh is None:
             return False
-        allocation.block_tables = tuple(
-            table + tuple(fresh[plane * extra : (plane + 1) * extra])
-            for plane, table in enumerate(allocation.block_tables)
-        )
+        allocation.block_tables = _widen(allocation.block_tables, fresh, extra)
         return True
 
     def free(self, request_id: str) -> None:
-        """Release a request's pages, or defer while a transfer holds them (:312-319)."""
+        """Release a request's pages, or defer while a transfer holds them (:312-319).
+
+        Pages go back table by table, each table from its last page to its first.
+        """
         allocation = self._allocations.get(request_id)
         if allocation is None:
             return
@@ -323,7 +416,7 @@ class KVPageBook:
             allocation.release_requested = True
             return
         del self._allocations[request_id]
-        self._drop_refs(b for table in allocation.block_tables for b in reversed(table))
+        self._pool.release(b for table in allocation.block_tables for b in reversed(table))
 
     def pin_transfer(self, request_id: str, transfer_id: str) -> None:
         allocation = self._get_allocation(request_id)
