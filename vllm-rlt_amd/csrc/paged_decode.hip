@@ -192,8 +192,22 @@ __device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, 
   const int pages = split_len / a.page;
   const int32_t* trow = a.tables + static_cast<int64_t>(r) * a.table_stride + sp * pages;
   const int32_t* shared = a.pg_pages + rec[kGroupPage0] + sp * pages;
+  // Entries in batches of 16 loads issued together: one memory round trip per
+  // batch rather than one per page.
+  constexpr int kBatch = 16;
   bool same = true;
-  for (int i = 0; i < pages; ++i) same &= trow[i] == shared[i];
+  int i = 0;
+  for (; i + kBatch <= pages; i += kBatch) {
+    int32_t tv[kBatch], gv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      tv[u] = trow[i + u];
+      gv[u] = shared[i + u];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) same &= tv[u] == gv[u];
+  }
+  for (; i < pages; ++i) same &= trow[i] == shared[i];
   return same;
 }
 
