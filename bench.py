@@ -992,9 +992,9 @@ def run_decode(args, name, device, with_cpu=True):
     prefix = w.prefix_hints is not None
     if w.fused_append and prefix:
         kernel = (
-            "rlt_paged_decode_shared_prefix with its append (shared_prefix_kernel over every plane's prefix + "
-            "paged_decode_kernel split pass reading each row's new token in place + paged_decode_merge_kernel "
-            "storing it)"
+            "rlt_paged_decode_shared_prefix with its append (paged_decode_prefix_kernel: prefix workers over "
+            "every plane's prefix beside the split pass reading each row's new token in place; "
+            "paged_decode_merge_kernel storing it)"
         )
     elif w.fused_append:
         kernel = (
@@ -1005,8 +1005,8 @@ def run_decode(args, name, device, with_cpu=True):
         kernel = "rlt_kv_append + rlt_paged_decode (paged_decode_kernel split pass + paged_decode_merge_kernel)"
     else:
         kernel = (
-            "rlt_kv_append + rlt_paged_decode_shared_prefix (shared_prefix_kernel + paged_decode_kernel split "
-            "pass + paged_decode_merge_kernel)"
+            "rlt_kv_append + rlt_paged_decode_shared_prefix (paged_decode_prefix_kernel: prefix workers + "
+            "split pass; paged_decode_merge_kernel)"
         )
     line = {
         "metric": "paged decode attn+KV append: HBM GB/s (% peak), loop-steps/s at Ouro-1.4B",

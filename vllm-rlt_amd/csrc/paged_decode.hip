@@ -67,6 +67,17 @@ constexpr int kWaves = 4;
 constexpr int kSplitTokens = RLT_DECODE_SPLIT_TOKENS;
 constexpr int kTile = RLT_DECODE_TILE;
 constexpr int kMaxSplits = 64;
+// Shared-prefix pass (head_dim 128): keys per tile, padded LDS rows
+// (conflict-light K and transposing V reads), LDS elements of a workgroup
+// (a K and a V tile per key half).
+constexpr int kPrefixBK = 32;
+constexpr int kPrefixKRow = 128 + 8, kPrefixVRow = 128 + 32;
+constexpr int kPrefixTileElems = 2 * kPrefixBK * (kPrefixKRow + kPrefixVRow);
+#ifndef RLT_DECODE_PREFIX_WORKERS
+#define RLT_DECODE_PREFIX_WORKERS 128
+#endif
+constexpr int kPrefixWorkers = RLT_DECODE_PREFIX_WORKERS;
+static_assert(kPrefixWorkers > 0 && kPrefixWorkers % 8 == 0, "whole rounds of the 8 XCDs");
 constexpr int kMaxRowsPerLaunch = 8192;
 #ifndef RLT_DECODE_MAX_GRID
 #define RLT_DECODE_MAX_GRID 4096
@@ -107,7 +118,6 @@ struct DecodeArgs {
   int64_t o_row, o_head, o_dim;
   float* ws_acc;  // [rows][hkv][kMaxSplits][G][D]
   float2* ws_ml;  // [rows][hkv][kMaxSplits][G]  (max in log2 units, sum)
-  uint8_t* ws_taken;  // [rows][kMaxSplits]: split taken by the prefix pass (written by it each launch)
   int n_rows, hkv, hq, d, page;
   int xcd_groups;  // > 0: XCD-affine schedule over this many (split, head block) groups
   int64_t num_blocks;
@@ -120,13 +130,18 @@ struct DecodeArgs {
   // its member rows and shared page ids are slices of pg_members / pg_pages;
   // pg_item_start[g] is the first prefix-pass work item of group g.  The
   // splits of a member row inside its group's pages (at the group's split
-  // length) come from shared_prefix_kernel instead of the split pass.
+  // length) come from the prefix workers (shared_prefix_item) instead of
+  // the split pass.
   const int32_t* pg_row_group;
   const int32_t* pg_groups;
   const int32_t* pg_item_start;
   const int32_t* pg_members;
   const int32_t* pg_pages;
   int pg_n_groups, pg_n_members, pg_n_pages, pg_n_items;
+  // Workgroups 0 .. pg_workers - 1 of the split pass compute the prefix
+  // pass's items (item w, w + pg_workers, ...) while the others stream the
+  // rest; a multiple of the XCD count, so the split pass's XCD mapping holds.
+  int pg_workers;
   // Fused KV append (rlt_paged_decode_append; null / 0 otherwise): row
   // r < n_write stores its new token k_new[r] / v_new[r] ([hkv, D], strides
   // in elements, dim stride 1) at slot (write_blocks[r], write_offsets[r]) of
@@ -179,13 +194,10 @@ __device__ __forceinline__ const int32_t* prefix_candidate(const DecodeArgs& a, 
   return rec;
 }
 
-// True when split sp of row r is computed by shared_prefix_kernel rather than
-// by the split pass: it is a candidate and the row's table holds exactly the
+// True when split sp of row r is computed by the prefix pass rather than by
+// the split pass: it is a candidate and the row's table holds exactly the
 // group's pages there.  All of it depends on the row and its own group only.
-// The prefix pass evaluates this for every (member row, candidate split) of
-// every group and records the answer in ws_taken; the split pass, which runs
-// after it, reads the record (prefix_taken) instead of comparing the pages
-// again, so every split is produced exactly once.
+// Both passes evaluate it, so every split is produced exactly once.
 __device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
   const int32_t* rec = prefix_candidate(a, r, sp, split_len, ns);
   if (!rec) return false;
@@ -209,12 +221,6 @@ __device__ bool prefix_takes(const DecodeArgs& a, int r, int sp, int split_len, 
   }
   for (; i < pages; ++i) same &= trow[i] == shared[i];
   return same;
-}
-
-// The split pass's side of prefix_takes: the prefix pass's record for a
-// candidate split.
-__device__ __forceinline__ bool prefix_taken(const DecodeArgs& a, int r, int sp, int split_len, int ns) {
-  return prefix_candidate(a, r, sp, split_len, ns) && a.ws_taken[static_cast<int64_t>(r) * kMaxSplits + sp] != 0;
 }
 
 // K/V page reads: each byte is read once per launch.
@@ -358,8 +364,14 @@ __device__ void merge_partials(const DecodeArgs& a, int r, int h, int j, int ns,
     if (live) store_elem(orow + (lane + dd * 64) * a.o_dim, acc[dd] * inv);
 }
 
+// The prefix pass's work item (defined with the prefix pass below).
+template <typename T, int G>
+__device__ __forceinline__ void shared_prefix_item(const DecodeArgs& a, int item, int h, uint16_t* tiles);
+
+// The split pass over workgroups block = 0 .. blocks - 1 of a 256-thread
+// launch (the kernels below map their workgroups onto it).
 template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX, bool APPEND>
-__global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const int blocks) {
   using PK = Packet<T>;
   constexpr int EPL = PK::N;      // elements of one token a lane owns
   constexpr int LPT = D / EPL;    // lanes per token
@@ -628,14 +640,16 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 
   if constexpr (XCD) {
     // XCD-affine schedule: workgroup b runs on XCD b % kXcds (the dispatcher's
-    // round-robin) and owns one (row, split, block of kWaves heads).  Groups
+    // round-robin; b counts from the first split-pass workgroup, after a whole
+    // number of rounds of prefix workers) and owns one (row, split, block of
+    // kWaves heads).  Groups
     // gi = split * head_blocks + block are dealt out in rounds of kXcds; in
     // round k XCD x serves group k * kXcds + (x - k) mod kXcds, so every XCD
     // takes early and late splits alike (later splits have fewer rows).  Each
     // XCD walks its groups in order with all rows of a group back to back, so
     // rows that alias the same pages in the same split read them together
     // from one L2.  Items past a row's split count exit at once.
-    const int b = blockIdx.x;
+    const int b = block;
     const int t = b / kXcds;
     const int r = t % a.n_rows;
     const int round = t / a.n_rows;
@@ -647,14 +661,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int len = uniform(row_length(a, r));
     int split_len, ns;
     split_plan(len, &split_len, &ns);
-    if (sp < ns && !(PREFIX && uniform(prefix_taken(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
+    if (sp < ns && !(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
   } else {
     // Packed schedule (any head count): the compact list of rows x splits x
     // kv heads, kv head innermost, walked in grid-stride order.
     extern __shared__ int prefix[];
     const int total_splits = build_split_prefix(a, prefix);
     const int total = total_splits * a.hkv;
-    for (int item = blockIdx.x * kWaves + wave; item < total; item += gridDim.x * kWaves) {
+    for (int item = block * kWaves + wave; item < total; item += blocks * kWaves) {
       const int qi = item / a.hkv;
       const int h = item - qi * a.hkv;
       const int r = uniform(find_row(prefix, a.n_rows, qi));
@@ -662,9 +676,29 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       const int len = uniform(row_length(a, r));
       int split_len, ns;
       split_plan(len, &split_len, &ns);
-      if (!(PREFIX && uniform(prefix_taken(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
+      if (!(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
     }
   }
+}
+
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool APPEND>
+__global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  split_pass<T, D, G, P, TILE, XCD, false, APPEND>(a, blockIdx.x, gridDim.x);
+}
+
+// The split pass with prefix groups: its first pg_workers workgroups compute
+// the prefix pass's items (w, w + pg_workers, ...) while the rest run the split
+// pass, which skips exactly the splits they take (prefix_takes, evaluated
+// alike on both sides).  Two waves per SIMD, as the prefix items need.
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool APPEND>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_prefix_kernel(DecodeArgs a) {
+  if (static_cast<int>(blockIdx.x) < a.pg_workers) {
+    __shared__ __align__(16) uint16_t tiles[kPrefixTileElems];
+    const int total = a.pg_n_items * a.hkv;
+    for (int w = blockIdx.x; w < total; w += a.pg_workers) shared_prefix_item<T, G>(a, w / a.hkv, w % a.hkv, tiles);
+    return;
+  }
+  split_pass<T, D, G, P, TILE, XCD, true, APPEND>(a, blockIdx.x - a.pg_workers, gridDim.x - a.pg_workers);
 }
 
 // Merge kernel: one wavefront per (row, kv_head) with more than one split;
@@ -713,9 +747,10 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 }
 
 // Shared-prefix pass: the split partials of the splits that prefix_takes()
-// gives it, for every group at once.  Work item i (blockIdx.x) belongs to the
+// gives it, for every group at once, computed by the first workgroups of the
+// split pass's launch (paged_decode_prefix_kernel).  Work item i belongs to the
 // group g with item_start[g] <= i < item_start[g + 1]; its offset in the group
-// is (split sp, block b of 64 queries), b fastest.  Workgroup (i, h) owns
+// is (split sp, block b of 64 queries), b fastest.  Item (i, h) owns
 // split sp of group g's pages (keys [sp * S, (sp + 1) * S), S the group's
 // split length) under kv head h, for 64 queries: (row, q head) pairs
 // b * 64 .. b * 64 + 63 of the group's members x G.  Wave w takes queries
@@ -733,24 +768,23 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 // share the workgroup (so not on the batch).  The result is written as the
 // split pass would: (max, sum) and the unnormalised accumulator in the decode
 // workspace slot of (row, h, sp).
-constexpr int kPrefixBK = 32;   // keys per tile
 constexpr float kPrefixRescale = 8.f;
 
-// Two waves per SIMD (at most 256 registers a lane, none spilled): one launch
-// round for 512 workgroups, where the latency-bound pass otherwise takes two.
+// Work item `item` of the prefix pass under kv head h, by the 256 threads of a
+// workgroup with `tiles` (kPrefixTileElems elements) of LDS.  Every thread of
+// the workgroup calls it with the same arguments; it leaves the LDS free for
+// the next call once all threads have passed its first barrier.
 template <typename T, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void shared_prefix_kernel(DecodeArgs a) {
+__device__ __forceinline__ void shared_prefix_item(const DecodeArgs& a, const int item, const int h, uint16_t* tiles) {
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   constexpr int D = 128, KSTEPS = D / 16, DTILES = D / 32;
-  constexpr int KROW = D + 8, VROW = D + 32;  // padded rows: conflict-light K and transposing V reads
+  constexpr int KROW = kPrefixKRow, VROW = kPrefixVRow;
   constexpr int KTILE = kPrefixBK * KROW, VTILE = kPrefixBK * VROW;
   constexpr int MERGE_FLOATS = 2 + 16 * DTILES;  // (max, sum, acc) per lane
   static_assert(2 * 64 * MERGE_FLOATS * 4 <= 2 * (KTILE + VTILE) * 2, "merge fits in the tile buffers");
-  __shared__ __align__(16) uint16_t tiles[2 * (KTILE + VTILE)];  // per key half: K tile, V tile
+  static_assert(kPrefixTileElems == 2 * (KTILE + VTILE), "tile buffer size");
 
-  const int item = blockIdx.x;
-  const int h = blockIdx.y;
   const int tid = threadIdx.x;
   // The item's group: the last g with item_start[g] <= item.
   int g = 0;
@@ -833,11 +867,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     int split_len, ns;
     split_plan(row_length(a, r), &split_len, &ns);
     mine = prefix_takes(a, r, sp, split_len, ns);
-    // The record the split pass reads: every (member, candidate split) pair is
-    // in exactly one item of its group, whose lanes of that member (one per
-    // q head of the KV head, for every KV head) all write the same value.
-    if (h == 0 && j == 0 && prefix_candidate(a, r, sp, split_len, ns))
-      a.ws_taken[static_cast<int64_t>(r) * kMaxSplits + sp] = mine ? 1 : 0;
   }
   if (!__syncthreads_or(mine)) return;
 
@@ -1030,12 +1059,22 @@ using DecodeKernel = void (*)(DecodeArgs);
 
 template <typename T, int D, bool XCD, bool PREFIX, bool APPEND>
 DecodeKernel pick_group(int G) {
-  switch (G) {
-    case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, PREFIX, APPEND>;
-    case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, PREFIX, APPEND>;
-    case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, PREFIX, APPEND>;
-    case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, PREFIX, APPEND>;
-    default: return nullptr;
+  if constexpr (PREFIX) {
+    switch (G) {
+      case 1: return paged_decode_prefix_kernel<T, D, 1, 16, kTile, XCD, APPEND>;
+      case 2: return paged_decode_prefix_kernel<T, D, 2, 16, kTile, XCD, APPEND>;
+      case 4: return paged_decode_prefix_kernel<T, D, 4, 16, kTile, XCD, APPEND>;
+      case 8: return paged_decode_prefix_kernel<T, D, 8, 16, kTile, XCD, APPEND>;
+      default: return nullptr;
+    }
+  } else {
+    switch (G) {
+      case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, APPEND>;
+      case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, APPEND>;
+      case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, APPEND>;
+      case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, APPEND>;
+      default: return nullptr;
+    }
   }
 }
 
@@ -1107,23 +1146,6 @@ __global__ __launch_bounds__(64) void slice_append_kernel(DecodeArgs a) {
 
 bool stride16(int64_t stride, int esize) { return (stride * esize) % 16 == 0; }
 
-// The shared-prefix pass for this shape, or null where it does not exist
-// (the caller then drops the hint and the split pass computes every split).
-template <typename T>
-DecodeKernel shared_prefix_pass(int d, int G) {
-  if constexpr (std::is_same_v<T, float>) {
-    return nullptr;
-  } else {
-    if (d != 128) return nullptr;
-    switch (G) {
-      case 1: return shared_prefix_kernel<T, 1>;
-      case 2: return shared_prefix_kernel<T, 2>;
-      case 4: return shared_prefix_kernel<T, 4>;
-      case 8: return shared_prefix_kernel<T, 8>;
-      default: return nullptr;
-    }
-  }
-}
 
 template <typename T>
 int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
@@ -1136,14 +1158,11 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
                          stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
                          a.kv_token * a.page < (int64_t(1) << 31);
   const bool xcd = RLT_DECODE_XCD_SCHEDULE && a.hkv % kWaves == 0;
-  // The prefix groups are served where the prefix pass and a split pass with
-  // the prefix check exist for this shape; elsewhere the hint is dropped.
-  const DecodeKernel prefix_pass =
-      (a.pg_row_group && a.pg_n_items > 0 && layout_ok && pick_tiled<T>(a.d, G, xcd, true, false))
-          ? shared_prefix_pass<T>(a.d, G)
-          : nullptr;
-  if (!prefix_pass) a.pg_row_group = nullptr;
-  const bool prefix = prefix_pass != nullptr;
+  // The prefix groups are served where the split pass with prefix workers
+  // exists for this shape (16-bit types, head_dim 128, 1/2/4/8 q heads per kv
+  // head); elsewhere the hint is dropped.
+  const bool prefix = a.pg_row_group && a.pg_n_items > 0 && layout_ok && pick_tiled<T>(a.d, G, xcd, true, false);
+  if (!prefix) a.pg_row_group = nullptr;
   if (a.n_write > 0) {
     // The fused append needs the tiled kernel and 16-byte rows of k_new / v_new;
     // otherwise the new tokens are written first and the decode runs as usual.
@@ -1159,11 +1178,11 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   const bool append = a.n_write > 0;
   if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, prefix, append);
   if (prefix) {
-    // The prefix splits are never a row's last split, which holds the new
-    // token, so the prefix pass reads no slot the fused append writes.
-    hipLaunchKernelGGL(prefix_pass, dim3(static_cast<unsigned>(a.pg_n_items), static_cast<unsigned>(a.hkv)),
-                       dim3(256), 0, stream, a);
-    if (int rc = check_launch("rlt_paged_decode_shared_prefix(prefix)")) return rc;
+    // The prefix pass's items run in the split pass's first workgroups.  The
+    // prefix splits are never a row's last split, which holds the new token,
+    // so they read no slot the fused append writes.
+    const int64_t items = static_cast<int64_t>(a.pg_n_items) * a.hkv;
+    a.pg_workers = static_cast<int>(std::min<int64_t>(kPrefixWorkers, (items + kXcds - 1) / kXcds * kXcds));
   }
   if (!tiled) {
     if (a.d > 64 * kGenericMaxPerLane) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: head_dim > 512");
@@ -1175,13 +1194,13 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   const int64_t splits_cap = std::min<int64_t>(kMaxSplits, (max_tokens + kSplitTokens - 1) / kSplitTokens);
   if (xcd) {
     const int64_t groups = std::max<int64_t>(splits_cap, 1) * (a.hkv / kWaves);
-    const int64_t grid = static_cast<int64_t>(kXcds) * a.n_rows * ((groups + kXcds - 1) / kXcds);
+    const int64_t grid = static_cast<int64_t>(kXcds) * a.n_rows * ((groups + kXcds - 1) / kXcds) + a.pg_workers;
     if (grid > 0x7fffffff) return fail(RLT_EUNSUPPORTED, "rlt_paged_decode: too many work items");
     a.xcd_groups = static_cast<int>(groups);
     hipLaunchKernelGGL(tiled, dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), 0, stream, a);
   } else {
     const int64_t items = static_cast<int64_t>(a.n_rows) * a.hkv * std::max<int64_t>(splits_cap, 1);
-    const int grid = static_cast<int>(std::min<int64_t>(kMaxGrid, (items + kWaves - 1) / kWaves));
+    const int grid = static_cast<int>(std::min<int64_t>(kMaxGrid, (items + kWaves - 1) / kWaves)) + a.pg_workers;
     const size_t lds = static_cast<size_t>(a.n_rows + 1) * sizeof(int);
     a.xcd_groups = 0;
     hipLaunchKernelGGL(tiled, dim3(grid), dim3(64 * kWaves), lds, stream, a);
@@ -1203,9 +1222,9 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
 
 int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Workspace layout: acc partials | (max, sum) partials | prefix-taken bytes.
+// Workspace layout: acc partials | (max, sum) partials.
 struct WorkspaceLayout {
-  int64_t acc, ml, taken, total;
+  int64_t acc, ml, total;
 };
 WorkspaceLayout workspace_layout(int64_t rows, int64_t hq, int64_t hkv, int64_t d) {
   rows = std::min<int64_t>(rows, kMaxRowsPerLaunch);
@@ -1213,8 +1232,7 @@ WorkspaceLayout workspace_layout(int64_t rows, int64_t hq, int64_t hkv, int64_t 
   WorkspaceLayout w{};
   w.acc = 0;
   w.ml = round256(slots * d * static_cast<int64_t>(sizeof(float)));
-  w.taken = w.ml + round256(slots * static_cast<int64_t>(sizeof(float2)));
-  w.total = w.taken + round256(rows * kMaxSplits);
+  w.total = w.ml + round256(slots * static_cast<int64_t>(sizeof(float2)));
   return w;
 }
 
@@ -1295,7 +1313,6 @@ int paged_decode(const void* q, const int64_t* q_strides, const void* key_cache,
   char* ws = static_cast<char*>(workspace);
   a.ws_acc = reinterpret_cast<float*>(ws + layout.acc);
   a.ws_ml = reinterpret_cast<float2*>(ws + layout.ml);
-  a.ws_taken = reinterpret_cast<uint8_t*>(ws + layout.taken);
   a.hkv = static_cast<int>(num_kv_heads);
   a.hq = static_cast<int>(num_q_heads);
   a.d = static_cast<int>(head_dim);
