@@ -107,14 +107,6 @@ __device__ __forceinline__ int lds_swizzle(int r) {
   return ((r >> 2) & 1) | ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r ^ (r >> 1) ^ (r >> 3)) & 1) << 3);
 }
 
-// x, as a value the compiler cannot see through: addresses derived from it
-// are recomputed where they are used (a few integer operations) instead of
-// being hoisted out of the tile loop, where they would hold registers.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kPage = 16;
@@ -547,7 +539,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
     const char* v_rows = reinterpret_cast<const char*>(group_lds + b_pv * (KT + VT) + KT);
     const char* k_rows = reinterpret_cast<const char*>(group_lds + b_s * (KT + VT));
-    const int vk = opaque(v_key), vk_hi = opaque(v_key_hi), kk = opaque(k_key);
+    const int vk = v_key, vk_hi = v_key_hi, kk = k_key;
     auto read = [&](int k) __attribute__((always_inline)) {
       if (k < 16) {
         const int ks = k >> 2, c = k & 3;
