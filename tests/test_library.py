@@ -91,6 +91,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert rc == native.RLT_EINVAL and "n_pages" in native.last_error()
     rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 1, 2, 32, -1, *tail)
     assert rc == native.RLT_EINVAL and "n_items" in native.last_error()
+    # Items x KV heads (16 here) must fit the workers' 32-bit item indices.
+    rc = lib.rlt_paged_decode_shared_prefix(*decode, *append, 1, 1, 2, 32, (1 << 31) // 16, *tail)
+    assert rc == native.RLT_EINVAL and "n_items x num_kv_heads" in native.last_error()
 
 
 def test_workspace_sizes_depend_only_on_shape():

@@ -1508,8 +1508,9 @@ extern "C" int rlt_paged_decode_shared_prefix(
     return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_members must be in [n_groups, n_rows]");
   if (n_pages < 1 || n_pages > n_groups * max_table_width)
     return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_pages must be in [1, n_groups x max_table_width]");
-  if (n_items < 0 || n_items > 0x7fffffff)
-    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_items out of range");
+  // The prefix workers walk n_items x num_kv_heads items in 32-bit indices.
+  if (n_items < 0 || n_items > 0x7fffffff / std::max<int64_t>(num_kv_heads, 1))
+    return fail(RLT_EINVAL, "rlt_paged_decode_shared_prefix: n_items x num_kv_heads out of range");
   const PrefixHint hint{prefix_groups, n_groups, n_members, n_pages, n_items};
   const AppendSource append{k_new, k_new_strides, v_new, v_new_strides, write_blocks, write_offsets, n_write};
   return paged_decode(q, q_strides, key_cache, value_cache, kv_strides, block_tables, table_stride, max_table_width,
