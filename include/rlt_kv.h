@@ -298,9 +298,9 @@ int64_t rlt_paged_decode_no_alloc_rows_per_launch(int64_t num_q_heads, int64_t n
  *     members[n_members]          the rows of every group, group after group;
  *     pages[n_pages]              the shared page ids of every group.
  *   n_items = item_start[n_groups], with n_items x num_kv_heads < 2^31.  The
- *   members of group g must be exactly
- *   the rows with row_group == g; the split length is the decode split plan's
- *   for the members (256 << k: a function of a row's length alone).
+ *   members of group g must be exactly the rows with row_group == g; the split
+ *   length is the decode split plan's for the members (256 << k: a function
+ *   of a row's length alone).
  * A member's splits inside its group's pages are computed once for all
  * members (bf16 or fp16, head_dim 128, q heads per KV head 1/2/4/8, page 16;
  * other shapes ignore the hint) and merged with each row's remaining splits.
