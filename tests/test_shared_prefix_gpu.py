@@ -134,6 +134,29 @@ def test_four_planes_of_prefixes_in_one_launch(hq, hkv):
     assert torch.equal(hinted[[5, 17, 9]], plain[[5, 17, 9]])
 
 
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 8)])
+def test_many_groups_in_one_launch(hq, hkv):
+    # 72 groups of two rows (prefixes of 16-40 pages, one row with no group per
+    # eight): the item -> group search walks many groups, and each of the
+    # launch's prefix workers computes several items in turn.
+    g = torch.Generator().manual_seed(hq + 5 * hkv)
+    groups = 72
+    group_pages = torch.randint(16, 41, (groups,), generator=g).tolist()
+    row_group = [r // 2 if r % 8 != 7 else -1 for r in range(2 * groups)]
+    lengths = [int(group_pages[grp] * PAGE + torch.randint(1, 700, (1,), generator=g)) if grp >= 0
+               else int(torch.randint(300, 1500, (1,), generator=g)) for grp in row_group]
+    case, _, hint_pages = groups_case(lengths, row_group, group_pages, hq=hq, hkv=hkv, seed=hq * 7 + hkv)
+    print(f"[prefix groups] {groups} groups hq={hq} hkv={hkv}", flush=True)
+    hint = hint_for(case, hint_pages)
+    assert hint.n_groups == len({grp for grp in row_group if grp >= 0})
+    assert hint.n_items * hkv > 128  # more items than prefix workers
+    hinted = run(case, hint_pages)
+    check(case, hinted)
+    plain = run(case)
+    ungrouped = [r for r, grp in enumerate(row_group) if grp < 0]
+    assert torch.equal(bits(hinted[ungrouped]), bits(plain[ungrouped]))
+
+
 @pytest.mark.parametrize("hq,hkv", [(16, 16), (16, 4)])
 def test_512_token_splits_beside_256_token_splits(hq, hkv):
     # Rows past 16384 tokens use 512-token splits: the same 600 shared pages
