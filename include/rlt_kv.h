@@ -217,7 +217,9 @@ int rlt_paged_decode(const void* q, const int64_t* q_strides, const void* key_ca
  * and the output equal that sequence's bit for bit.  Inside the launch a row
  * whose write slot is its own last token's slot (table[(len-1)/page],
  * (len-1) % page) reads that token from k_new / v_new, and the pages are
- * written after every split has read its keys.  So the caller guarantees that
+ * written after every split has read its keys (when max_table_width x
+ * page_size <= 256 every row is one split, which stores its row's token
+ * after its own reads, and no merge kernel runs).  So the caller guarantees that
  * no row reads a slot another row writes in this launch (true of a decode
  * batch with one row per request and depth; a packed chunk, where a row reads
  * the tokens of the rows before it, must use rlt_kv_append then

@@ -89,6 +89,40 @@ def test_fused_append_equals_two_steps_and_the_oracle(dtype, hq, hkv, d):
     check_against_oracle(case, k_new, v_new, blocks, offsets, n, *got)
 
 
+SHORT = [1, 15, 16, 17, 120, 200, 255, 256]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 16, 128), (16, 4, 128), (8, 8, 64), (4, 2, 128)])
+def test_tables_of_one_split_store_the_token_in_the_split_pass(dtype, hq, hkv, d):
+    # Tables of at most 256 tokens: every row is one split, the split pass
+    # writes the outputs and stores the new tokens itself, and no merge runs.
+    case, k_new, v_new, blocks, offsets, n = decode_batch(SHORT, hq=hq, hkv=hkv, d=d, dtype=dtype, seed=hq + d + 3)
+    assert case.tables.shape[1] * 16 <= 256
+    print(f"[decode_append] one split {dtype} hq={hq} hkv={hkv} d={d}", flush=True)
+    ref = two_step(case, k_new, v_new, blocks, offsets, n)
+    got = fused(case, k_new, v_new, blocks, offsets, n)
+    for a, b in zip(got, ref):
+        assert torch.equal(bits(a), bits(b))
+    check_against_oracle(case, k_new, v_new, blocks, offsets, n, *got)
+
+
+def test_one_split_tables_with_empty_rows_and_a_slot_nobody_reads():
+    # An empty row that appends (to a page no table reads) and pad rows past
+    # n_write, in a launch where every row is one split.
+    lengths = [40, 0, 90, 256, 0, 0]
+    case, k_new, v_new, blocks, offsets, n = decode_batch(lengths, hq=16, hkv=16, d=128, dtype=torch.bfloat16,
+                                                          seed=17, n_write=4)
+    spare = sorted(set(range(case.key_pool.shape[0])) - set(case.tables.flatten().tolist()))[0]
+    blocks[1], offsets[1] = spare, 5
+    ref = two_step(case, k_new, v_new, blocks, offsets, n)
+    got = fused(case, k_new, v_new, blocks, offsets, n)
+    for a, b in zip(got, ref):
+        assert torch.equal(bits(a), bits(b))
+    assert torch.count_nonzero(got[0][[1, 4, 5]]) == 0
+    check_against_oracle(case, k_new, v_new, blocks, offsets, n, *got)
+
+
 def test_fused_append_with_a_stale_workspace():
     # The merge kernel reads the new token from a clamped row and every split slot
     # before it knows the row's split count; a NaN-filled workspace (what earlier

@@ -148,7 +148,8 @@ struct DecodeArgs {
   // the layer slices.  The split pass reads a row's own new token from
   // k_new / v_new (its last token, when the write slot is the row's last
   // token slot) and the merge kernel stores it into the pages after every
-  // split has read them, so no page is written and read in one kernel.
+  // split has read them (in a single-split launch the row's one item stores
+  // it after its own reads), so no slot is written before it is read.
   const void* k_new;
   const void* v_new;
   int64_t kn_row, kn_head, kn_dim, vn_row, vn_head, vn_dim;
@@ -369,8 +370,11 @@ template <typename T, int G>
 __device__ __forceinline__ void shared_prefix_item(const DecodeArgs& a, int item, int h, uint16_t* tiles);
 
 // The split pass over workgroups block = 0 .. blocks - 1 of a 256-thread
-// launch (the kernels below map their workgroups onto it).
-template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX, bool APPEND>
+// launch (the kernels below map their workgroups onto it).  ONE_SPLIT: every
+// row is a single split (the tables span at most one split), so each row's one
+// item stores the row's new token itself (APPEND), after its own reads, and no
+// merge kernel runs.
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool PREFIX, bool APPEND, bool ONE_SPLIT = false>
 __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const int blocks) {
   using PK = Packet<T>;
   constexpr int EPL = PK::N;      // elements of one token a lane owns
@@ -388,6 +392,24 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
   const int s = lane % LPT;
   const uint32_t lane_dim = static_cast<uint32_t>(s * EPL);
 
+  // A one-split launch's append: row r's new token of kv head h into its
+  // write slot (skipped when the slot is outside the pool), by the lanes of
+  // one token, after the item has read its pages.
+  auto store_new_token = [&](const int r, const int h) {
+    if constexpr (APPEND && ONE_SPLIT) {
+      if (r >= a.n_write || g != 0) return;
+      const int64_t b = a.write_blocks[r], o = a.write_offsets[r];
+      if (b < 0 || b >= a.num_blocks || o < 0 || o >= a.page) return;
+      const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head + lane_dim;
+      const u32x4 kt = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + r * a.kn_row +
+                                                        static_cast<int64_t>(h) * a.kn_head + lane_dim);
+      const u32x4 vt = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + r * a.vn_row +
+                                                        static_cast<int64_t>(h) * a.vn_head + lane_dim);
+      *reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.k)) + slot) = kt;
+      *reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.v)) + slot) = vt;
+    }
+  };
+
   // One (row r, kv head h, split sp) item per wave.
   auto process = [&](const int r, const int h, const int sp, const int len, const int split_len, const int ns) {
     if (len <= 0) {
@@ -397,6 +419,7 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
 #pragma unroll
         for (int j = 0; j < G; ++j) *reinterpret_cast<u32x4*>(orow + j * a.o_head) = zero;
       }
+      store_new_token(r, h);
       return;
     }
     const int t_begin = sp * split_len;
@@ -615,6 +638,7 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
           *reinterpret_cast<u32x4*>(orow + j * a.o_head) = PK::pack(o);
         }
       }
+      store_new_token(r, h);
     } else {
       const int64_t slot = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits + sp;
       if (g == 0) {
@@ -681,9 +705,9 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
   }
 }
 
-template <typename T, int D, int G, int P, int TILE, bool XCD, bool APPEND>
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool APPEND, bool ONE_SPLIT>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
-  split_pass<T, D, G, P, TILE, XCD, false, APPEND>(a, blockIdx.x, gridDim.x);
+  split_pass<T, D, G, P, TILE, XCD, false, APPEND, ONE_SPLIT>(a, blockIdx.x, gridDim.x);
 }
 
 // The split pass with prefix groups: its first pg_workers workgroups compute
@@ -1057,7 +1081,7 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
 // Host dispatch.
 using DecodeKernel = void (*)(DecodeArgs);
 
-template <typename T, int D, bool XCD, bool PREFIX, bool APPEND>
+template <typename T, int D, bool XCD, bool PREFIX, bool APPEND, bool ONE_SPLIT = false>
 DecodeKernel pick_group(int G) {
   if constexpr (PREFIX) {
     switch (G) {
@@ -1069,10 +1093,10 @@ DecodeKernel pick_group(int G) {
     }
   } else {
     switch (G) {
-      case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, APPEND>;
-      case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, APPEND>;
-      case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, APPEND>;
-      case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, APPEND>;
+      case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+      case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+      case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+      case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, APPEND, ONE_SPLIT>;
       default: return nullptr;
     }
   }
@@ -1081,47 +1105,53 @@ DecodeKernel pick_group(int G) {
 // The fused-append split pass is compiled for the XCD-affine schedule (with
 // and without the shared-prefix check); other cases append first, then decode.
 template <typename T, int D, bool PREFIX>
-DecodeKernel pick_group(int G, bool xcd, bool append) {
-  if (append) return xcd ? pick_group<T, D, true, PREFIX, true>(G) : nullptr;
+DecodeKernel pick_group(int G, bool xcd, bool append, bool one_split) {
+  if (append) {
+    if (!xcd) return nullptr;
+    if constexpr (!PREFIX) {
+      if (one_split) return pick_group<T, D, true, false, true, true>(G);
+    }
+    return pick_group<T, D, true, PREFIX, true>(G);
+  }
   return xcd ? pick_group<T, D, true, PREFIX, false>(G) : pick_group<T, D, false, PREFIX, false>(G);
 }
 
 // The split pass with the shared-prefix check exists where the prefix pass
 // does (16-bit types, head_dim 128); everywhere else it is compiled out.
 template <typename T, int D>
-DecodeKernel pick_group(int G, bool xcd, bool prefix, bool append) {
+DecodeKernel pick_group(int G, bool xcd, bool prefix, bool append, bool one_split) {
   if (prefix) {
-    if constexpr (D == 128 && !std::is_same_v<T, float>) return pick_group<T, D, true>(G, xcd, append);
+    if constexpr (D == 128 && !std::is_same_v<T, float>) return pick_group<T, D, true>(G, xcd, append, one_split);
     return nullptr;
   }
-  return pick_group<T, D, false>(G, xcd, append);
+  return pick_group<T, D, false>(G, xcd, append, one_split);
 }
 
 template <typename T>
-DecodeKernel pick_tiled(int d, int G, bool xcd, bool prefix, bool append);
+DecodeKernel pick_tiled(int d, int G, bool xcd, bool prefix, bool append, bool one_split = false);
 template <>
-DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd, bool prefix, bool append) {
+DecodeKernel pick_tiled<bf16>(int d, int G, bool xcd, bool prefix, bool append, bool one_split) {
   switch (d) {
-    case 64: return pick_group<bf16, 64>(G, xcd, prefix, append);
-    case 128: return pick_group<bf16, 128>(G, xcd, prefix, append);
-    case 256: return pick_group<bf16, 256>(G, xcd, prefix, append);
+    case 64: return pick_group<bf16, 64>(G, xcd, prefix, append, one_split);
+    case 128: return pick_group<bf16, 128>(G, xcd, prefix, append, one_split);
+    case 256: return pick_group<bf16, 256>(G, xcd, prefix, append, one_split);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<f16>(int d, int G, bool xcd, bool prefix, bool append) {
+DecodeKernel pick_tiled<f16>(int d, int G, bool xcd, bool prefix, bool append, bool one_split) {
   switch (d) {
-    case 64: return pick_group<f16, 64>(G, xcd, prefix, append);
-    case 128: return pick_group<f16, 128>(G, xcd, prefix, append);
-    case 256: return pick_group<f16, 256>(G, xcd, prefix, append);
+    case 64: return pick_group<f16, 64>(G, xcd, prefix, append, one_split);
+    case 128: return pick_group<f16, 128>(G, xcd, prefix, append, one_split);
+    case 256: return pick_group<f16, 256>(G, xcd, prefix, append, one_split);
     default: return nullptr;
   }
 }
 template <>
-DecodeKernel pick_tiled<float>(int d, int G, bool xcd, bool prefix, bool append) {
+DecodeKernel pick_tiled<float>(int d, int G, bool xcd, bool prefix, bool append, bool one_split) {
   switch (d) {
-    case 64: return pick_group<float, 64>(G, xcd, prefix, append);
-    case 128: return pick_group<float, 128>(G, xcd, prefix, append);
+    case 64: return pick_group<float, 64>(G, xcd, prefix, append, one_split);
+    case 128: return pick_group<float, 128>(G, xcd, prefix, append, one_split);
     default: return nullptr;
   }
 }
@@ -1158,10 +1188,16 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
                          stride16(a.kv_block, esize) && stride16(a.kv_token, esize) && stride16(a.kv_head, esize) &&
                          a.kv_token * a.page < (int64_t(1) << 31);
   const bool xcd = RLT_DECODE_XCD_SCHEDULE && a.hkv % kWaves == 0;
+  // A table of at most one split's tokens makes every row a single split:
+  // the split pass then writes every output itself and no merge runs.
+  const int64_t max_tokens = max_table_width * a.page;
+  const bool single_split = max_tokens <= kSplitTokens;
   // The prefix groups are served where the split pass with prefix workers
   // exists for this shape (16-bit types, head_dim 128, 1/2/4/8 q heads per kv
-  // head); elsewhere the hint is dropped.
-  const bool prefix = a.pg_row_group && a.pg_n_items > 0 && layout_ok && pick_tiled<T>(a.d, G, xcd, true, false);
+  // head) and rows span more than one split (a prefix split is never a row's
+  // last); elsewhere the hint is dropped.
+  const bool prefix = a.pg_row_group && a.pg_n_items > 0 && layout_ok && !single_split &&
+                      pick_tiled<T>(a.d, G, xcd, true, false);
   if (!prefix) a.pg_row_group = nullptr;
   if (a.n_write > 0) {
     // The fused append needs the tiled kernel and 16-byte rows of k_new / v_new;
@@ -1176,7 +1212,8 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
     }
   }
   const bool append = a.n_write > 0;
-  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, prefix, append);
+  // One-split rows: each row's one item stores its new token after its reads.
+  if (layout_ok) tiled = pick_tiled<T>(a.d, G, xcd, prefix, append, single_split);
   if (prefix) {
     // The prefix pass's items run in the split pass's first workgroups.  The
     // prefix splits are never a row's last split, which holds the new token,
@@ -1190,7 +1227,6 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
     hipLaunchKernelGGL(paged_decode_generic_kernel<T>, dim3(a.n_rows, a.hq), dim3(64), 0, stream, a);
     return check_launch("rlt_paged_decode(generic)");
   }
-  const int64_t max_tokens = max_table_width * a.page;
   const int64_t splits_cap = std::min<int64_t>(kMaxSplits, (max_tokens + kSplitTokens - 1) / kSplitTokens);
   if (xcd) {
     const int64_t groups = std::max<int64_t>(splits_cap, 1) * (a.hkv / kWaves);
@@ -1206,6 +1242,7 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
     hipLaunchKernelGGL(tiled, dim3(grid), dim3(64 * kWaves), lds, stream, a);
   }
   if (int rc = check_launch("rlt_paged_decode")) return rc;
+  if (single_split) return RLT_OK;
   const int merge_grid = (a.n_rows * a.hkv + kWaves - 1) / kWaves;
   const dim3 mgrid(merge_grid), mblock(64 * kWaves);
   if (append) {
