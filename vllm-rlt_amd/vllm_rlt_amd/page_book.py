@@ -144,6 +144,8 @@ class _PagePool:
 
     def take(self, count: int) -> list:
         """The top `count` pages of the stack, top first, each now held once."""
+        if not 0 <= count <= len(self.free):
+            raise AssertionError(f"cannot take {count} of {len(self.free)} free pages")
         cut = len(self.free) - count
         pages = self.free[cut:][::-1]
         del self.free[cut:]
