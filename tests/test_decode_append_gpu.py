@@ -78,7 +78,8 @@ LENGTHS = [1, 15, 16, 17, 255, 256, 257, 300, 600, 1029, 4100, 9000]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("hq,hkv,d", [(16, 16, 128), (32, 16, 128), (16, 4, 128), (8, 8, 64), (4, 4, 256), (4, 2, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 16, 128), (32, 16, 128), (16, 4, 128), (8, 8, 64), (4, 4, 256), (4, 2, 128),
+                                     (32, 4, 128), (64, 8, 64)])
 def test_fused_append_equals_two_steps_and_the_oracle(dtype, hq, hkv, d):
     case, k_new, v_new, blocks, offsets, n = decode_batch(LENGTHS, hq=hq, hkv=hkv, d=d, dtype=dtype, seed=hq + d)
     print(f"[decode_append] {dtype} hq={hq} hkv={hkv} d={d}", flush=True)
@@ -93,7 +94,7 @@ SHORT = [1, 15, 16, 17, 120, 200, 255, 256]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("hq,hkv,d", [(16, 16, 128), (16, 4, 128), (8, 8, 64), (4, 2, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 16, 128), (16, 4, 128), (8, 8, 64), (4, 2, 128), (32, 4, 128)])
 def test_tables_of_one_split_store_the_token_in_the_split_pass(dtype, hq, hkv, d):
     # Tables of at most 256 tokens: every row is one split, the split pass
     # writes the outputs and stores the new tokens itself, and no merge runs.

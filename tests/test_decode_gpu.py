@@ -42,7 +42,7 @@ def assert_close(actual, case):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("hq,hkv", [(16, 16), (8, 4), (16, 4), (16, 2)])
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (8, 4), (16, 4), (16, 2), (32, 8), (32, 4), (64, 8)])
 def test_tiled_decode_matches_oracle(dtype, hq, hkv):
     case = random_decode_case(LENGTHS, hq=hq, hkv=hkv, d=128, dtype=dtype, seed=hq * 31 + hkv)
     assert_close(run_hip(case), case)
