@@ -285,6 +285,33 @@ def test_mfma_prefill_empty_and_single_token_sequences(dtype):
     torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 16, 128), (4, 2, 64)])
+def test_mfma_prefill_context_shorter_than_chunk(dtype, hq, hkv, d):
+    # Query row i of a chunk sees context_length - (chunk - 1 - i) keys, none
+    # when that is not positive: such rows are zeros, like the per-token
+    # oracle's zero-length rows -- including whole 128-row query tiles that see
+    # nothing (chunk 300 over 20 keys: rows 0-279), and a sequence with no keys.
+    from vllm_rlt_amd import ops
+
+    chunks, contexts = [300, 200, 5, 40], [20, 0, 3, 40]
+    q, kp, vp, tables, _, cu, row_tables, _ = ragged_prefill_case(dtype, hq, hkv, d, [0] * 4, chunks, 31)
+    row_lengths = torch.tensor(
+        [max(0, n - (c - 1 - i)) for n, c in zip(contexts, chunks) for i in range(c)], dtype=torch.int32
+    )
+    print(f"[prefill short context] chunks={chunks} contexts={contexts} hq={hq} d={d} {dtype}", flush=True)
+    out = torch.full_like(q, 7.0).cuda()
+    ops.paged_prefill(
+        q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), torch.tensor(contexts, dtype=torch.int32).cuda(),
+        cu.cuda(), max(chunks), out=out,
+    )
+    torch.cuda.synchronize()
+    expect = paged_attention_cpu(q, kp, vp, row_tables, row_lengths)
+    assert torch.count_nonzero(out.cpu()[row_lengths == 0]) == 0
+    atol, rtol = TOL[dtype]
+    torch.testing.assert_close(out.cpu(), expect, atol=atol, rtol=rtol)
+
+
 @pytest.mark.parametrize("num_seqs", [137, 512, 513])
 def test_mfma_prefill_many_sequences(num_seqs):
     # The ranked work list sorts and scans the sequences in the workgroup (up to

@@ -265,7 +265,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int qt0 = t * kBM;                         // first chunk row of the workgroup
   const int wg_last_row = min(qt0 + kBM, nq) - 1;  // last chunk row of the workgroup
   const int wg_keys = prefix + wg_last_row + 1;    // <= len_k, so len_k >= 1 below
-  if (wg_keys <= 0) return;
+  if (wg_keys <= 0) {
+    // No row of the tile sees a key (a context shorter than its chunk): the
+    // rows are written as zeros, as a row that sees no key is below.
+    constexpr int CH = D / 8;  // 16-byte chunks per row
+    const int rows = wg_last_row + 1 - qt0;
+    for (int i = tid; i < rows * CH; i += 512) {
+      T* orow = static_cast<T*>(a.out) + (row0 + qt0 + i / CH) * a.o_row + static_cast<int64_t>(h) * a.o_head;
+      *reinterpret_cast<u32x4*>(orow + (i % CH) * 8) = u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
   const int ntiles = (wg_keys + kBN - 1) / kBN;
 
   // Waves 0-3 take key tiles 0, 2, 4, ...; waves 4-7 tiles 1, 3, 5, ...; wave
