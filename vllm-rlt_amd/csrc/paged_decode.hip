@@ -73,6 +73,9 @@ constexpr int kMaxSplits = 64;
 constexpr int kPrefixBK = 32;
 constexpr int kPrefixKRow = 128 + 8, kPrefixVRow = 128 + 32;
 constexpr int kPrefixTileElems = 2 * kPrefixBK * (kPrefixKRow + kPrefixVRow);
+// A query's running maximum (prefix pass, grouped-query split pass) moves only
+// when a tile exceeds it by more than this many powers of two.
+constexpr float kPrefixRescale = 8.f;
 #ifndef RLT_DECODE_PREFIX_WORKERS
 #define RLT_DECODE_PREFIX_WORKERS 128
 #endif
@@ -662,6 +665,232 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
     }
   };
 
+  // Grouped-query items (4 or 8 q heads per kv head, head_dim 128, page 16,
+  // 16-bit types) on the matrix cores instead.  Per 32-token tile the wave
+  // loads the K and V rows four whole rows per instruction and stages them in
+  // its own LDS rows, one after the other.  It forms S^T = K Q^T with
+  // v_mfma_f32_32x32x16 (A = K from the staged rows: lane (token c, half)
+  // reads dims 16ks + 8half .. + 7 of row c; B = q, column c being q head
+  // c % G, so columns G..31 repeat the heads and are dropped), keeps an online
+  // softmax per column in log2 units (the running maximum moves only by more
+  // than 2^kPrefixRescale), and accumulates O^T += V^T P^T with P rounded to T
+  // and V^T from transposing reads of the staged V rows; the row sums come from
+  // the same P (v_dot2 against ones).  Loads of tile t + 1 go out while tile t
+  // computes (K after its scores, V after its staging).  Same partials,
+  // outputs and fused-append handling as `process`.
+  constexpr bool kMfma = (G == 4 || G == 8) && D == 128 && P == 16 && !std::is_same_v<T, float>;
+  constexpr int kMfmaTile = 32;
+  // Each wave's staged rows: a tile's K rows (kPrefixKRow apart), then its V
+  // rows over them (kPrefixVRow apart).
+  __shared__ __align__(16) uint16_t gqa_rows[kMfma ? kWaves * kMfmaTile * kPrefixVRow : 1];
+  auto process_mfma = [&](const int r, const int h, const int sp, const int len, const int split_len, const int ns) {
+    if constexpr (kMfma) {
+      using Ops = MfmaOps<T>;
+      using V8 = typename Ops::V8;
+      constexpr int BK = kMfmaTile, KSTEPS = D / 16, DTILES = D / 32, VROW = kPrefixVRow;
+      if (len <= 0) {  // a row with no keys is written as zeros
+        if (g == 0) {
+          T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h) * G * a.o_head + lane_dim;
+          const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int jj = 0; jj < G; ++jj) *reinterpret_cast<u32x4*>(orow + jj * a.o_head) = zero;
+        }
+        store_new_token(r, h);
+        return;
+      }
+      const int t_begin = sp * split_len;
+      const int t_end = min(len, t_begin + split_len);
+      const int last = t_end - 1;
+      int64_t wb = -1, wo = -1;
+      if constexpr (APPEND) {
+        if (t_end == len && r < a.n_write) {
+          wb = a.write_blocks[r];
+          wo = a.write_offsets[r];
+        }
+      }
+      const int half = lane >> 5;
+      const int col = lane & 31;
+      const int j = col % G;
+      uint16_t* const rows_lds = gqa_rows + wave * BK * VROW;
+
+      u32x4 qb[KSTEPS];
+      {
+        const T* qrow = static_cast<const T*>(a.q) + r * a.q_row + static_cast<int64_t>(h * G + j) * a.q_head;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 16 + half * 8);
+      }
+      const int grp = lane >> 4, gl = lane & 15;
+      const int tr_off = (4 * (grp >> 1) + (gl >> 2)) * VROW + 16 * (grp & 1) + 4 * (gl & 3);
+      f32x16 acc_o[DTILES];
+#pragma unroll
+      for (int c = 0; c < DTILES; ++c) acc_o[c] = f32x16{};
+      // This lane's share of its column's row sum (the lane 32 away holds the
+      // other keys), from the same rounded P that weights V.
+      float lsum = 0.f;
+      float m = -INFINITY;
+
+      const int32_t* trow = a.tables + r * a.table_stride;
+      const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.kv_head;
+      const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.kv_head;
+      const T* kn_row = nullptr;
+      const T* vn_row = nullptr;
+      if constexpr (APPEND) {
+        kn_row = static_cast<const T*>(a.k_new) + r * a.kn_row + static_cast<int64_t>(h) * a.kn_head;
+        vn_row = static_cast<const T*>(a.v_new) + r * a.vn_row + static_cast<int64_t>(h) * a.vn_head;
+      }
+      const uint32_t tok_stride = static_cast<uint32_t>(a.kv_token);
+
+      constexpr int kChunkTokens = 64 * P;  // one table entry per lane
+      for (int c0 = t_begin; c0 < t_end; c0 += kChunkTokens) {
+        const int c1 = min(t_end, c0 + kChunkTokens);
+        const int chunk_page = c0 / P;
+        const int chunk_last = (c1 - 1) / P - chunk_page;  // <= 63
+        const int table_entry = lane <= chunk_last ? trow[chunk_page + lane] : 0;
+        // The row's new token comes from k_new / v_new when this chunk ends
+        // the row and the write slot is its last token's slot.
+        bool fresh = false;
+        if constexpr (APPEND)
+          fresh = c1 == len && wb >= 0 && wo == (len - 1) % P &&
+                  wb == static_cast<int64_t>(__builtin_amdgcn_readlane(table_entry, chunk_last));
+        // Pages of the tile at t0 (two 16-token pages), clamped into the pool.
+        auto tile_blocks = [&](int t0, int64_t& b0, int64_t& b1) {
+          const int rel = (t0 - c0) / P;
+          const int64_t x0 = __builtin_amdgcn_readlane(table_entry, min(rel, chunk_last));
+          const int64_t x1 = __builtin_amdgcn_readlane(table_entry, min(rel + 1, chunk_last));
+          b0 = (x0 < 0 || x0 >= a.num_blocks) ? 0 : x0;
+          b1 = (x1 < 0 || x1 >= a.num_blocks) ? 0 : x1;
+        };
+        // Token t of the tile at t0 (clamped to the split's last token) at
+        // element offset dim: its page slot, or k_new / v_new for a fresh token.
+        auto src = [&](const T* base, const T* fresh_row, int64_t b0, int64_t b1, int t0, int t, int dim) {
+          const int tok = min(t, last);
+          const int64_t blk = ((tok - t0) >> 4) ? b1 : b0;
+          const T* p = base + blk * a.kv_block + static_cast<uint32_t>(tok & (P - 1)) * tok_stride + dim;
+          if constexpr (APPEND) {
+            if (fresh && tok == len - 1) p = fresh_row + dim;
+          }
+          return reinterpret_cast<const u32x4*>(p);
+        };
+        // K and V rows in natural layout: lane (row (lane >> 4) + 4i, chunk
+        // lane & 15), four whole rows per load.
+        auto load_rows = [&](u32x4 (&rows)[BK / 4], const T* base, const T* fresh_row, int t0) {
+          int64_t b0, b1;
+          tile_blocks(t0, b0, b1);
+#pragma unroll
+          for (int i = 0; i < BK / 4; ++i)
+            rows[i] = load_page(src(base, fresh_row, b0, b1, t0, t0 + (lane >> 4) + 4 * i, (lane & 15) * 8));
+        };
+        auto stage_rows = [&](const u32x4 (&rows)[BK / 4], int stride) {
+#pragma unroll
+          for (int i = 0; i < BK / 4; ++i)
+            *reinterpret_cast<u32x4*>(&rows_lds[((lane >> 4) + 4 * i) * stride + (lane & 15) * 8]) = rows[i];
+        };
+        const int ntiles = (c1 - c0 + BK - 1) / BK;
+        u32x4 kt[BK / 4], vt[BK / 4];
+        load_rows(kt, kbase, kn_row, c0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_rows(vt, vbase, vn_row, c0);
+        for (int it = 0; it < ntiles; ++it) {
+          const int t0 = c0 + it * BK;
+          // K goes through the wave's LDS rows into operand layout (the
+          // previous tile's V reads of those rows were issued before, and LDS
+          // runs one wave's operations in order).
+          stage_rows(kt, kPrefixKRow);
+          u32x4 ka[KSTEPS];
+#pragma unroll
+          for (int ks = 0; ks < KSTEPS; ++ks)
+            ka[ks] = *reinterpret_cast<const u32x4*>(&rows_lds[col * kPrefixKRow + ks * 16 + half * 8]);
+          f32x16 sacc = f32x16{};
+#pragma unroll
+          for (int ks = 0; ks < KSTEPS; ++ks) sacc = Ops::mma(as_v8<V8>(ka[ks]), as_v8<V8>(qb[ks]), sacc);
+          if (it + 1 < ntiles) load_rows(kt, kbase, kn_row, t0 + BK);
+          __builtin_amdgcn_sched_barrier(0);
+          // Element e of this lane is token t0 + 8(e/4) + 4half + e%4.
+          float tmax = -INFINITY;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const bool valid = t0 + 8 * (e >> 2) + 4 * half + (e & 3) <= last;
+            sacc[e] = valid ? sacc[e] * a.qscale : -INFINITY;
+            tmax = fmaxf(tmax, sacc[e]);
+          }
+          tmax = max_across_halves(tmax);
+          const bool move = tmax > m + kPrefixRescale;
+          if (__builtin_amdgcn_ballot_w64(move) != 0) {
+            const float mn = move ? fmaxf(m, tmax) : m;
+            const float corr = (!move || mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+#pragma unroll
+            for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc_o[c][e] *= corr;
+            lsum *= corr;
+            m = mn;
+          }
+          const float mb = (m == -INFINITY) ? 0.f : m;
+          u32x4 pb[2];
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              pb[ks][e] = Ops::pack2(fast_exp2(sacc[ks * 8 + 2 * e] - mb), fast_exp2(sacc[ks * 8 + 2 * e + 1] - mb));
+          // Stage this tile's V over its K rows (read above), then send the
+          // next tile's V loads.
+          stage_rows(vt, VROW);
+          if (it + 1 < ntiles) load_rows(vt, vbase, vn_row, t0 + BK);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int c = 0; c < DTILES; ++c) {
+              const uint16_t* vlo = &rows_lds[tr_off + ks * 16 * VROW + c * 32];
+              const u32x2 lo = lds_read_tr(vlo);
+              const u32x2 hi = lds_read_tr(vlo + 8 * VROW);
+              const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
+              acc_o[c] = Ops::mma(as_v8<V8>(va), as_v8<V8>(pb[ks]), acc_o[c]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) lsum = Ops::sum2(pb[ks][e], lsum);
+          }
+        }
+      }
+
+      // Columns 0 .. G-1 hold the q heads.  O^T element e of dim tile c is dim
+      // 32c + 8(e/4) + 4half + e%4.
+      const float l = lsum + __shfl_xor(lsum, 32, 64);
+      if (col < G) {
+        if (ns == 1) {
+          T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head + 4 * half;
+          const float inv = 1.f / l;
+#pragma unroll
+          for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const u32x2 w2 = {Ops::pack2(acc_o[c][4 * g4] * inv, acc_o[c][4 * g4 + 1] * inv),
+                                Ops::pack2(acc_o[c][4 * g4 + 2] * inv, acc_o[c][4 * g4 + 3] * inv)};
+              *reinterpret_cast<u32x2*>(orow + 32 * c + 8 * g4) = w2;
+            }
+        } else {
+          const int64_t slot = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits + sp;
+          float* dst = a.ws_acc + (slot * G + j) * D + 4 * half;
+#pragma unroll
+          for (int c = 0; c < DTILES; ++c)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              u32x4 w;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(acc_o[c][4 * g4 + e]);
+              *reinterpret_cast<u32x4*>(dst + 32 * c + 8 * g4) = w;
+            }
+          if (half == 0) a.ws_ml[slot * G + j] = make_float2(m, l);
+        }
+      }
+      if (ns == 1) store_new_token(r, h);
+    }
+  };
+  auto run_item = [&](const int r, const int h, const int sp, const int len, const int split_len, const int ns) {
+    if constexpr (kMfma) process_mfma(r, h, sp, len, split_len, ns);
+    else process(r, h, sp, len, split_len, ns);
+  };
+
   if constexpr (XCD) {
     // XCD-affine schedule: workgroup b runs on XCD b % kXcds (the dispatcher's
     // round-robin; b counts from the first split-pass workgroup, after a whole
@@ -685,7 +914,7 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
     const int len = uniform(row_length(a, r));
     int split_len, ns;
     split_plan(len, &split_len, &ns);
-    if (sp < ns && !(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
+    if (sp < ns && !(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) run_item(r, h, sp, len, split_len, ns);
   } else {
     // Packed schedule (any head count): the compact list of rows x splits x
     // kv heads, kv head innermost, walked in grid-stride order.
@@ -700,13 +929,20 @@ __device__ __forceinline__ void split_pass(DecodeArgs a, const int block, const 
       const int len = uniform(row_length(a, r));
       int split_len, ns;
       split_plan(len, &split_len, &ns);
-      if (!(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) process(r, h, sp, len, split_len, ns);
+      if (!(PREFIX && uniform(prefix_takes(a, r, sp, split_len, ns)))) run_item(r, h, sp, len, split_len, ns);
     }
   }
 }
 
 template <typename T, int D, int G, int P, int TILE, bool XCD, bool APPEND, bool ONE_SPLIT>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  split_pass<T, D, G, P, TILE, XCD, false, APPEND, ONE_SPLIT>(a, blockIdx.x, gridDim.x);
+}
+
+// The split pass for the grouped-query items on the matrix cores (4 or 8 q
+// heads per kv head, head_dim 128, 16-bit types), held to two waves per SIMD.
+template <typename T, int D, int G, int P, int TILE, bool XCD, bool APPEND, bool ONE_SPLIT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_gqa_kernel(DecodeArgs a) {
   split_pass<T, D, G, P, TILE, XCD, false, APPEND, ONE_SPLIT>(a, blockIdx.x, gridDim.x);
 }
 
@@ -792,8 +1028,6 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 // share the workgroup (so not on the batch).  The result is written as the
 // split pass would: (max, sum) and the unnormalised accumulator in the decode
 // workspace slot of (row, h, sp).
-constexpr float kPrefixRescale = 8.f;
-
 // Work item `item` of the prefix pass under kv head h, by the 256 threads of a
 // workgroup with `tiles` (kPrefixTileElems elements) of LDS.  Every thread of
 // the workgroup calls it with the same arguments; it leaves the LDS free for
@@ -1092,11 +1326,16 @@ DecodeKernel pick_group(int G) {
       default: return nullptr;
     }
   } else {
+    constexpr bool kMfmaGroups = D == 128 && !std::is_same_v<T, float>;  // split_pass's grouped-query items
     switch (G) {
       case 1: return paged_decode_kernel<T, D, 1, 16, kTile, XCD, APPEND, ONE_SPLIT>;
       case 2: return paged_decode_kernel<T, D, 2, 16, kTile, XCD, APPEND, ONE_SPLIT>;
-      case 4: return paged_decode_kernel<T, D, 4, 16, kTile, XCD, APPEND, ONE_SPLIT>;
-      case 8: return paged_decode_kernel<T, D, 8, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+      case 4:
+        if constexpr (kMfmaGroups) return paged_decode_gqa_kernel<T, D, 4, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+        return paged_decode_kernel<T, D, 4, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+      case 8:
+        if constexpr (kMfmaGroups) return paged_decode_gqa_kernel<T, D, 8, 16, kTile, XCD, APPEND, ONE_SPLIT>;
+        return paged_decode_kernel<T, D, 8, 16, kTile, XCD, APPEND, ONE_SPLIT>;
       default: return nullptr;
     }
   }
