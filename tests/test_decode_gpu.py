@@ -102,11 +102,13 @@ def test_stale_workspace_slots_never_reach_the_output():
     assert_close(out.cpu(), case.to("cpu"))
 
 
-def test_rows_are_batch_invariant():
-    # tests/test_flash_attention.py:193-208: a row's bits do not depend on the batch around it.
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (32, 4)])
+def test_rows_are_batch_invariant(hq, hkv):
+    # tests/test_flash_attention.py:193-208: a row's bits do not depend on the batch around it
+    # (also for the grouped-query items on the matrix cores).
     from vllm_rlt_amd import ops
 
-    case = random_decode_case([1025, 1029, 1025, 1031, 3, 4000], d=128, seed=1234).to("cuda")
+    case = random_decode_case([1025, 1029, 1025, 1031, 3, 4000], hq=hq, hkv=hkv, d=128, seed=1234).to("cuda")
     together = ops.paged_decode(case.q, case.key_slice, case.value_slice, case.tables, case.lengths)
     for rows in ([2, 3], [3, 0], [1], [5, 4, 0]):
         idx = torch.tensor(rows, device="cuda")

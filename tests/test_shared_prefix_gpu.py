@@ -98,7 +98,7 @@ def bits(t):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("hq,hkv", [(16, 16), (8, 4), (16, 4), (16, 2)])
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (8, 4), (16, 4), (16, 2), (32, 4)])
 def test_one_group_with_256_token_splits(dtype, hq, hkv):
     # 40 shared pages (640 tokens, two whole 256-token splits).  Members: longer
     # than the prefix, shorter than it, a single split (not served), empty; row
@@ -134,7 +134,7 @@ def test_four_planes_of_prefixes_in_one_launch(hq, hkv):
     assert torch.equal(hinted[[5, 17, 9]], plain[[5, 17, 9]])
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 8)])
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 8), (32, 4)])
 def test_many_groups_in_one_launch(hq, hkv):
     # 72 groups of two rows (prefixes of 16-40 pages, one row with no group per
     # eight): the item -> group search walks many groups, and each of the
