@@ -56,6 +56,15 @@ def test_tiled_decode_long_rows_many_splits(d):
     assert_close(run_hip(case), case)
 
 
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (32, 4)])
+def test_grouped_query_rows_past_65536_tokens(hq, hkv):
+    # Rows past 65536 tokens get 2048-token splits, which the grouped-query
+    # items on the matrix cores walk in several 64-page table chunks.
+    case = random_decode_case([70000, 131072, 5000, 0], hq=hq, hkv=hkv, d=128, dtype=torch.bfloat16, seed=hq + hkv)
+    print(f"[decode long gqa] hq={hq} hkv={hkv}", flush=True)
+    assert_close(run_hip(case), case)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [64, 256])
 def test_tiled_decode_other_head_dims(dtype, d):
