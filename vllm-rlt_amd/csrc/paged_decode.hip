@@ -961,9 +961,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   split_pass<T, D, G, P, TILE, XCD, true, APPEND>(a, blockIdx.x - a.pg_workers, gridDim.x - a.pg_workers);
 }
 
-// Merge kernel: one wavefront per (row, kv_head) with more than one split;
-// with a fused append (APPEND) also the page write of every appending (row,
-// kv_head): 16-byte chunks of the [D] slab from k_new / v_new to
+// Merge kernel: one wavefront per (row, q head) of a row with more than one
+// split (the q heads of one kv head in parallel); with a fused append (APPEND)
+// the wave of each (row, kv_head)'s first q head also writes that row's new
+// token for the kv head: 16-byte chunks of the [D] slab from k_new / v_new to
 // (write_blocks[r], write_offsets[r]), skipped when the slot is outside the
 // pool.  All loads go out before the first wait: the row's length, the write
 // slot and the new token (read from a clamped row and chunk, so no load needs
@@ -975,9 +976,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int kChunks = D * static_cast<int>(sizeof(T)) / 16;
   static_assert(kChunks <= 64 && 64 % kChunks == 0, "whole chunks per lane group");
   const int item = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (item >= a.n_rows * a.hkv) return;
-  const int r = item / a.hkv;
-  const int h = item - r * a.hkv;
+  if (item >= a.n_rows * a.hq) return;
+  const int G = a.hq / a.hkv;
+  const int r = item / a.hq;
+  const int qh = item - r * a.hq;
+  const int h = qh / G;
+  const int j = qh - h * G;
   const int lane = threadIdx.x & 63;
   const int len = row_length(a, r);
   int64_t b = -1, o = -1;
@@ -992,14 +996,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     vt = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + rw * a.vn_row +
                                         static_cast<int64_t>(h) * a.vn_head)[chunk];
   }
-  const MergeLoads<D> first = load_partials<D>(a, r, h, 0, lane);
+  const MergeLoads<D> first = load_partials<D>(a, r, h, j, lane);
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
   int split_len, ns;
   split_plan(len, &split_len, &ns);
-  merge_partials<T, D>(a, r, h, 0, ns, lane, first);
-  if (ns > 1)
-    for (int j = 1; j < a.hq / a.hkv; ++j) merge_partials<T, D>(a, r, h, j, ns, lane, load_partials<D>(a, r, h, j, lane));
-  if (APPEND && r < a.n_write && lane < kChunks && b >= 0 && b < a.num_blocks && o >= 0 && o < a.page) {
+  merge_partials<T, D>(a, r, h, j, ns, lane, first);
+  if (APPEND && j == 0 && r < a.n_write && lane < kChunks && b >= 0 && b < a.num_blocks && o >= 0 && o < a.page) {
     const int64_t slot = b * a.kv_block + o * a.kv_token + static_cast<int64_t>(h) * a.kv_head;
     reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.k) + slot))[lane] = kt;
     reinterpret_cast<u32x4*>(const_cast<T*>(static_cast<const T*>(a.v) + slot))[lane] = vt;
@@ -1482,7 +1484,7 @@ int launch_decode(DecodeArgs a, int64_t max_table_width, hipStream_t stream) {
   }
   if (int rc = check_launch("rlt_paged_decode")) return rc;
   if (single_split) return RLT_OK;
-  const int merge_grid = (a.n_rows * a.hkv + kWaves - 1) / kWaves;
+  const int merge_grid = (a.n_rows * a.hq + kWaves - 1) / kWaves;
   const dim3 mgrid(merge_grid), mblock(64 * kWaves);
   if (append) {
     if (a.d == 64) hipLaunchKernelGGL((paged_decode_merge_kernel<T, 64, true>), mgrid, mblock, 0, stream, a);
