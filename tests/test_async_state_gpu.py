@@ -10,7 +10,6 @@ across replays with eager work in between.
 
 from types import SimpleNamespace
 
-import numpy as np
 import pytest
 import torch
 

@@ -4,8 +4,6 @@ Scenarios follow the reference's manager tests (cited per test); attention is
 compared with the dense SDPA oracle, KV movement with exact equality.
 """
 
-import math
-
 import pytest
 import torch
 
