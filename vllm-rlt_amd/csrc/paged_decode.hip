@@ -292,87 +292,94 @@ __device__ __forceinline__ int find_row(const int* prefix, int n, int x) {
   return lo;
 }
 
-// Merges the split partials of (row r, kv head h) into the output when the
-// row has ns >= 2 splits.  Lane sp holds split sp's (max, sum) (kMaxSplits ==
-// 64 == wave size), so the global max and the normaliser are two wave
-// reductions; lane l sums dims l, l + 64, ... over splits in split order.  The
-// (max, sum) of all 64 slots and the first batch of accumulators (all of the
-// lane's dims for up to 64 / (D / 64) splits) are loaded whatever ns is --
-// every slot lies inside the workspace -- and the slots past ns are selected
-// away afterwards, so none of these loads waits for the row's length: the
-// merge costs one round trip to memory for the common split counts.  The
-// result depends only on the row's own partials.
+// Merges the split partials of (row r, kv head h, q head j) into the output
+// when the row has ns >= 2 splits.  Lane sp holds split sp's (max, sum)
+// (kMaxSplits == 64 == wave size), so the global max and the normaliser are
+// two wave reductions.  The accumulators are read 16 bytes per lane: lane
+// (q, c) of a load reads dims 4c .. 4c + 3 of split i * SPI + q, so one load
+// instruction covers SPI whole splits.  Each lane sums its splits in split
+// order, then the SPI lanes of one chunk are added by a fixed butterfly, so
+// the result depends only on the row's own partials.  The (max, sum) of all
+// 64 slots and the first batch of SPB splits are loaded whatever ns is (every
+// slot lies inside the workspace) and the slots past ns are selected away
+// afterwards, so none of these loads waits for the row's length: the merge
+// costs one round trip to memory for the common split counts.
 template <int D>
 struct MergeLoads {
-  static constexpr int DPL = D / 64;    // dims per lane
-  static constexpr int SPB = 64 / DPL;  // splits per load batch
+  static constexpr int CH = D / 4;     // 16-byte chunks of one split's accumulators
+  static constexpr int SPI = 64 / CH;  // splits per load instruction
+  // The first batch covers 16 splits (rows up to 4096 tokens at 256-token
+  // splits): a larger one reads more slots past ns than a second round trip
+  // for the longer rows costs.  Later batches cover up to 16 loads' worth.
+  static constexpr int SPB = 16;
+  static constexpr int NB = SPB / SPI;
+  static constexpr int NB2 = (kMaxSplits - SPB) / SPI < 16 ? (kMaxSplits - SPB) / SPI : 16;
+  static constexpr int FB = NB2 * SPI;  // splits per later batch: 48, 32, 16 for D = 64, 128, 256
   float2 ml;                            // this lane's split's (max, sum)
-  float x[DPL][SPB];                    // the first batch of accumulators
+  u32x4 x[NB];                          // the first batch of accumulators
 };
 
-// The (max, sum) of all 64 split slots of (row r, kv head h, query j) and the
-// first batch of accumulators: every slot lies inside the workspace, so they
-// load whatever the row's split count is.
 template <int D>
 __device__ __forceinline__ MergeLoads<D> load_partials(const DecodeArgs& a, int r, int h, int j, int lane) {
   using L = MergeLoads<D>;
+  static_assert(D % 64 == 0 && D <= 256 && L::SPB % L::SPI == 0 && L::SPB <= kMaxSplits, "whole chunks and splits");
   const int G = a.hq / a.hkv;
   const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
   const int64_t split_stride = static_cast<int64_t>(G) * D;
-  const float* base = a.ws_acc + (slot0 * G + j) * D + lane;
+  const float* base = a.ws_acc + (slot0 * G + j) * D + 4 * (lane % L::CH) + (lane / L::CH) * split_stride;
   L v;
   v.ml = a.ws_ml[(slot0 + lane) * G + j];
 #pragma unroll
-  for (int u = 0; u < L::SPB; ++u)
-#pragma unroll
-    for (int dd = 0; dd < L::DPL; ++dd) v.x[dd][u] = base[u * split_stride + dd * 64];
+  for (int i = 0; i < L::NB; ++i) v.x[i] = *reinterpret_cast<const u32x4*>(base + i * L::SPI * split_stride);
   return v;
 }
 
 template <typename T, int D>
 __device__ void merge_partials(const DecodeArgs& a, int r, int h, int j, int ns, int lane, MergeLoads<D> v) {
+  using L = MergeLoads<D>;
   // ns < 2: nothing to merge (the split pass wrote the row); only the store is skipped, so the
   // loads of v stay unconditional.
   const bool live = ns > 1;
   static_assert(kMaxSplits == 64, "one lane per split");
-  static_assert(D % 64 == 0 && D <= 256, "dims per lane");
-  constexpr int DPL = MergeLoads<D>::DPL;
-  constexpr int SPB = MergeLoads<D>::SPB;
   const int G = a.hq / a.hkv;
   const int64_t slot0 = (static_cast<int64_t>(r) * a.hkv + h) * kMaxSplits;
   const int64_t split_stride = static_cast<int64_t>(G) * D;
+  const int c = lane % L::CH, q = lane / L::CH;
   T* orow = static_cast<T*>(a.out) + r * a.o_row + static_cast<int64_t>(h * G + j) * a.o_head;
-  const float* base = a.ws_acc + (slot0 * G + j) * D + lane;
+  const float* base = a.ws_acc + (slot0 * G + j) * D + 4 * c + q * split_stride;
   const float2 ml = lane < ns ? v.ml : make_float2(-INFINITY, 0.f);
   const float M = strided_max<1>(ml.x);
   const float w = lane < ns ? fast_exp2(ml.x - M) : 0.f;
   const float inv = 1.f / group_sum<64>(ml.y * w);
-  float acc[DPL];
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int dd = 0; dd < DPL; ++dd) acc[dd] = 0.f;
-#pragma unroll
-  for (int u = 0; u < SPB; ++u) {
+  for (int i = 0; i < L::NB; ++i) {
+    const int u = i * L::SPI + q;
     const float wu = __shfl(w, u, 64);
 #pragma unroll
-    for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(u < ns ? v.x[dd][u] : 0.f, wu, acc[dd]);
+    for (int e = 0; e < 4; ++e) acc[e] = fmaf(u < ns ? __uint_as_float(v.x[i][e]) : 0.f, wu, acc[e]);
   }
-  // Further splits (long rows), a whole batch of loads in flight at a time.
-  for (int sp0 = SPB; live && sp0 < ns; sp0 += SPB) {
-    float x[DPL][SPB];
+  // Further splits (rows of more than SPB splits), a whole batch of loads in flight at a time.
+  for (int sp0 = L::SPB; live && sp0 < ns; sp0 += L::FB) {
+    u32x4 x[L::NB2];
 #pragma unroll
-    for (int u = 0; u < SPB; ++u)
+    for (int i = 0; i < L::NB2; ++i) {
+      const int u = sp0 + i * L::SPI + q;
+      x[i] = u < ns ? *reinterpret_cast<const u32x4*>(base + (sp0 + i * L::SPI) * split_stride) : u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
-      for (int dd = 0; dd < DPL; ++dd) x[dd][u] = sp0 + u < ns ? base[(sp0 + u) * split_stride + dd * 64] : 0.f;
+    for (int i = 0; i < L::NB2; ++i) {
+      const float wu = __shfl(w, (sp0 + i * L::SPI + q) & 63, 64);
 #pragma unroll
-    for (int u = 0; u < SPB; ++u) {
-      const float wu = __shfl(w, (sp0 + u) & 63, 64);
-#pragma unroll
-      for (int dd = 0; dd < DPL; ++dd) acc[dd] = fmaf(x[dd][u], wu, acc[dd]);
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(__uint_as_float(x[i][e]), wu, acc[e]);
     }
   }
 #pragma unroll
-  for (int dd = 0; dd < DPL; ++dd)
-    if (live) store_elem(orow + (lane + dd * 64) * a.o_dim, acc[dd] * inv);
+  for (int e = 0; e < 4; ++e) acc[e] = strided_sum<L::CH>(acc[e]);
+  if (live && q == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_elem(orow + (4 * c + e) * a.o_dim, acc[e] * inv);
+  }
 }
 
 // The prefix pass's work item (defined with the prefix pass below).
