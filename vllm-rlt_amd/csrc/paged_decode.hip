@@ -310,11 +310,12 @@ struct MergeLoads {
   static constexpr int SPI = 64 / CH;  // splits per load instruction
   // The first batch covers 16 splits (rows up to 4096 tokens at 256-token
   // splits): a larger one reads more slots past ns than a second round trip
-  // for the longer rows costs.  Later batches cover up to 16 loads' worth.
+  // for the longer rows costs.  Later batches take up to 24 loads per lane,
+  // so rows of up to 64 splits need one more round trip at D = 64 or 128.
   static constexpr int SPB = 16;
   static constexpr int NB = SPB / SPI;
-  static constexpr int NB2 = (kMaxSplits - SPB) / SPI < 16 ? (kMaxSplits - SPB) / SPI : 16;
-  static constexpr int FB = NB2 * SPI;  // splits per later batch: 48, 32, 16 for D = 64, 128, 256
+  static constexpr int NB2 = (kMaxSplits - SPB) / SPI < 24 ? (kMaxSplits - SPB) / SPI : 24;
+  static constexpr int FB = NB2 * SPI;  // splits per later batch: 48, 48, 24 for D = 64, 128, 256
   float2 ml;                            // this lane's split's (max, sum)
   u32x4 x[NB];                          // the first batch of accumulators
 };
