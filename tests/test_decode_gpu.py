@@ -56,6 +56,23 @@ def test_tiled_decode_long_rows_many_splits(d):
     assert_close(run_hip(case), case)
 
 
+# Split counts at the merge's load-batch edges: the first batch holds 16 splits,
+# later batches 48 (head_dim 64 and 128) or 24 (head_dim 256).
+MERGE_EDGE_SPLITS = [1, 2, 15, 16, 17, 40, 47, 48, 49, 63, 64]
+
+
+@pytest.mark.parametrize(
+    "d,dtype,hq,hkv",
+    [(64, torch.bfloat16, 4, 4), (128, torch.bfloat16, 4, 4), (256, torch.bfloat16, 4, 4),
+     (64, torch.float32, 4, 4), (128, torch.float32, 2, 2), (128, torch.bfloat16, 16, 4)],
+)
+def test_merge_batch_edges(d, dtype, hq, hkv):
+    lengths = [200 if ns == 1 else ns * 256 - 7 * ns % 256 for ns in MERGE_EDGE_SPLITS]
+    case = random_decode_case(lengths, hq=hq, hkv=hkv, d=d, dtype=dtype, seed=d + hq)
+    print(f"[merge edges] d={d} dtype={dtype} hq={hq} hkv={hkv}", flush=True)
+    assert_close(run_hip(case), case)
+
+
 @pytest.mark.parametrize("hq,hkv", [(16, 4), (32, 4)])
 def test_grouped_query_rows_past_65536_tokens(hq, hkv):
     # Rows past 65536 tokens get 2048-token splits, which the grouped-query
