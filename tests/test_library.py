@@ -124,3 +124,13 @@ def test_ops_refuse_cpu_tensors():
         hip_paged_attention(q, cache, cache, tables, lengths)
     with pytest.raises(ValueError, match="ROCm"):
         HipPagedAttention(torch.device("cpu"), torch.bfloat16, 128, 16)
+
+
+def test_int64_arrays_are_shared_by_value():
+    from vllm_rlt_amd import _native
+
+    strides = _native.int64_array((2048, 128, 1))
+    assert _native.int64_array([2048, 128, 1]) is strides
+    assert list(strides) == [2048, 128, 1]
+    assert list(_native.int64_array(list(range(20)))) == list(range(20))
+    assert list(_native.int64_array([])) == []

@@ -8,6 +8,7 @@ library is missing every operation raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_void_p
 from pathlib import Path
 
@@ -168,8 +169,19 @@ def check(rc: int, name: str) -> None:
     raise RuntimeError(message)
 
 
+@functools.lru_cache(maxsize=1024)
+def _short_int64_array(values: tuple) -> ctypes.Array:
+    return (c_int64 * len(values))(*values)
+
+
 def int64_array(values) -> ctypes.Array:
-    values = [int(v) for v in values]
+    """A C int64 array holding `values`.  Short ones (tensor strides) are built
+    once per distinct value and shared between calls: every entry point takes
+    them as `const int64_t*` and only reads them."""
+    if type(values) is not tuple:  # tensor strides already are tuples of ints
+        values = tuple(int(v) for v in values)
+    if len(values) <= 8:
+        return _short_int64_array(values)
     return (c_int64 * len(values))(*values)
 
 
@@ -180,5 +192,12 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise ValueError("KV dtype must be float32, float16, or bfloat16") from None
 
 
+# The current stream's raw handle without building a Stream object per call.
+_raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The HIP stream torch currently issues to on `device`."""
+    if _raw_current_stream is not None:
+        return _raw_current_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
